@@ -1,0 +1,214 @@
+"""SBDA attention benchmark: 20-layer forward+backward at T=2^20, H=8, D=64, bf16.
+
+One step = for every SBDA layer l = 1..20 (offsets (0, 2^(l-1)) for l <= 2,
+(0, 1, 2, 2^(l-1)) after): the fused forward (O + per-row LSE) and the fused
+backward (dQ, dK, dV) of one synthetic q/k/v/dO set (N(0,1), seeded, bf16,
+[B, T, H, D] memory seen as [B, H, T, D] views, as BiAttn/left_v2.py:240-244
+passes them).  Inputs are resident in HBM before timing starts.
+
+Prints one JSON line: positions/s (value), achieved algorithmic HBM GB/s and
+its fraction of MI355X's 8 TB/s, per-entry-point kernel times measured with
+HIP events on the launch stream, and the CPU baseline (the oracle's eager
+restatement of left_v2's gather path, fp32, timed on this host on a bounded
+sample).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "SBDA attn fwd+bwd positions/s and achieved HBM GB/s at T=1M, D=64, bf16"
+
+
+def sbda_offsets(layer: int) -> tuple[int, ...]:
+    jump = 1 << (layer - 1)
+    return (0, jump) if layer <= 2 else (0, 1, 2, jump)
+
+
+def algorithmic_bytes(rows: int, d: int, esz: int) -> tuple[int, int]:
+    """Per-launch ideal HBM bytes: forward reads q,k,v and writes o + fp32 LSE;
+    backward reads q,k,v,dO + LSE and writes dq,dk,dv."""
+    fwd = rows * (4 * d * esz + 4)
+    bwd = rows * (7 * d * esz + 4)
+    return fwd, bwd
+
+
+def cpu_baseline(layers: int, h: int, d: int, seconds_target: float = 15.0) -> dict:
+    """Time the oracle's fp32 eager path (fwd + autograd bwd) on this host."""
+    import torch
+    from oracle import sbda_oracle as ref
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    try:
+        torch.set_num_interop_threads(1)
+    except RuntimeError:
+        pass
+
+    def run(t: int) -> float:
+        g = torch.Generator().manual_seed(7)
+        q, k, v, go = (torch.randn(1, t, h, d, generator=g).permute(0, 2, 1, 3) for _ in range(4))
+        q.requires_grad_()
+        k.requires_grad_()
+        v.requires_grad_()
+        start = time.perf_counter()
+        for layer in range(1, layers + 1):
+            out = ref.gather_attention(q, k, v, sbda_offsets(layer))
+            out.backward(go)
+        return time.perf_counter() - start
+
+    t = 4096
+    elapsed = run(t)
+    # Grow the sample until one 20-layer pass takes a sizeable share of the target.
+    while elapsed < seconds_target / 4 and t < (1 << 20):
+        t *= 2
+        elapsed = run(t)
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    pos_s = t / elapsed
+    fwd_b, bwd_b = algorithmic_bytes(t * h, d, 4)
+    return {
+        "value": pos_s,
+        "unit": "positions/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle eager gather path (BiAttn/left_v2.py:313-405 restated), fp32, "
+                   f"B=1 T={t} H={h} D={d}, 20-layer SBDA fwd+bwd, one pass of {elapsed:.2f} s "
+                   f"on {threads} threads ({model})"),
+        "gbs_fp32_algorithmic": (fwd_b + bwd_b) * layers / elapsed / 1e9,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--length", type=int, default=1 << 20)
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--heads", type=int, default=8)
+    ap.add_argument("--head-dim", type=int, default=64)
+    ap.add_argument("--layers", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the op shards over batch/heads with no exchange; see DESIGN.md).",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    from __graft_entry__ import load_package
+
+    sbda = load_package()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    b, t, h, d, layers = args.batch, args.length, args.heads, args.head_dim, args.layers
+    dtype = torch.bfloat16
+    gen = torch.Generator(device=dev).manual_seed(2024)
+    q, k, v, go = (torch.randn(b, t, h, d, generator=gen, device=dev, dtype=torch.float32)
+                   .to(dtype).permute(0, 2, 1, 3) for _ in range(4))
+    offsets = [sbda_offsets(l) for l in range(1, layers + 1)]
+    stream = torch.cuda.current_stream(dev)
+
+    fwd_ev, bwd_ev = [], []
+
+    def step(record: bool) -> None:
+        for offs in offsets:
+            if record:
+                e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+                e0.record(stream)
+            out, lse = sbda.sbda_forward(q, k, v, offs)
+            if record:
+                e1.record(stream)
+            sbda.sbda_backward(q, k, v, go, lse, offs)
+            if record:
+                e2.record(stream)
+                fwd_ev.append((e0, e1))
+                bwd_ev.append((e1, e2))
+
+    for _ in range(args.warmup):
+        step(False)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+        step(True)
+    end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    ms_step = total_ms / args.steps
+    fwd_ms = sum(a.elapsed_time(z) for a, z in fwd_ev) / len(fwd_ev)
+    bwd_ms = sum(a.elapsed_time(z) for a, z in bwd_ev) / len(bwd_ev)
+
+    rows = b * h * t
+    fwd_b, bwd_b = algorithmic_bytes(rows, d, 2)
+    step_bytes = (fwd_b + bwd_b) * layers
+    gbs = step_bytes / (ms_step * 1e-3) / 1e9
+    positions_s = b * t / (ms_step * 1e-3)
+    bwd_gbs = bwd_b / (bwd_ms * 1e-3) / 1e9
+    fwd_gbs = fwd_b / (fwd_ms * 1e-3) / 1e9
+    dominant = "backward" if bwd_ms >= fwd_ms else "forward"
+
+    result = {
+        "metric": METRIC,
+        "value": positions_s,
+        "unit": "positions/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) q/k/v/dO, seeded, resident in HBM",
+        "config": {"workload": f"SBDA attention fwd+bwd, {layers}-layer dyadic schedule",
+                   "batch": b, "length": t, "heads": h, "head_dim": d,
+                   "layout": "[B,T,H,D] memory as [B,H,T,D] views"},
+        "achieved_gbs": gbs,
+        "hbm_fraction": gbs / HBM_PEAK_GBS,
+        "forward_ms_per_layer": fwd_ms,
+        "backward_ms_per_layer": bwd_ms,
+        "forward_gbs": fwd_gbs,
+        "backward_gbs": bwd_gbs,
+        "roofline": {
+            "bound": "hbm",
+            "kernel": f"sbda_{dominant} (all kernels of the entry point)",
+            "achieved": bwd_gbs if dominant == "backward" else fwd_gbs,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": (bwd_gbs if dominant == "backward" else fwd_gbs) / HBM_PEAK_GBS,
+            "traffic": None,
+            "algorithmic_bytes_per_launch": bwd_b if dominant == "backward" else fwd_b,
+        },
+        "cpu_baseline": None,
+    }
+    del q, k, v, go
+    torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(layers, h, d)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

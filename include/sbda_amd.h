@@ -1,0 +1,150 @@
+/*
+ * C ABI of the MI355X SBDA attention library (libsbda_amd.so, gfx950).
+ *
+ * Plain pointers and sizes only.  Every tensor is a [B, heads, T, D] view
+ * given by a device pointer and four element strides {b, h, t, d}; the d
+ * stride must be 1, the pointer 16-byte aligned and the b/h/t strides
+ * multiples of 16 bytes.  Offsets are host int32 arrays (S in 1..4, each
+ * >= 0).  `stream` is a hipStream_t (NULL = default stream).  Kernels are
+ * enqueued asynchronously on `stream`; nothing allocates device memory.
+ *
+ * Reference interfaces replaced (paths relative to the reference checkout,
+ * HaoyangMaLabs/Staged-Binary-Local-Diffusion-Attention v0.1.3):
+ *   sbda_forward            -> BiAttn/sbda_triton.py:1294-1327, the forward of
+ *                              _FusedSBDAKeyBackward (its two Triton launches
+ *                              _sbda_block_forward_kernel + _sbda_weights_kernel
+ *                              at :1312-1325).  Saves one fp32 log-normaliser
+ *                              per row instead of the [B,H,T,S] weight table.
+ *   sbda_backward           -> BiAttn/sbda_triton.py:1329-1360, the backward
+ *                              (launches _sbda_dq_from_weights_kernel and
+ *                              _sbda_dkv_key_kernel at :1342-1359); also the
+ *                              GQA pair at :1363-1434 when kv_heads < heads.
+ *   sbda_forward_prologue   -> BiAttn/left_v2.py:237-239 (q_norm, k_norm,
+ *                              _apply_rope from BiAttn/attention_common.py:
+ *                              25-50,64-76) fused into sbda_forward.
+ *   sbda_backward_prologue  -> the autograd backward of the same three ops
+ *                              fused into sbda_backward, plus the norm-weight
+ *                              gradients.
+ *   sbda_rope_table         -> BiAttn/attention_common.py:13-22
+ *                              (_rope_cos_sin), as a [T, D/2] device table.
+ *
+ * Return codes: SBDA_OK, or an error whose text sbda_last_error() returns
+ * (thread-local).  SBDA_ERR_VALUE maps to Python ValueError, SBDA_ERR_DTYPE to
+ * TypeError, SBDA_ERR_RUNTIME (a HIP error) to RuntimeError -- the error
+ * classes the reference's fused path raises (sbda_triton.py:1295-1302).
+ */
+#ifndef SBDA_AMD_H
+#define SBDA_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SBDA_OK 0
+#define SBDA_ERR_VALUE 1
+#define SBDA_ERR_DTYPE 2
+#define SBDA_ERR_RUNTIME 3
+
+#define SBDA_DTYPE_BF16 0
+#define SBDA_DTYPE_FP16 1
+#define SBDA_DTYPE_FP32 2
+
+/* ABI version of this header (bumped on any signature change). */
+int sbda_abi_version(void);
+
+/* Text of the last error on the calling thread ("" if none). */
+const char* sbda_last_error(void);
+
+/*
+ * Forward.  q: [B,H,T,D]; k, v: [B,Hkv,T,D] (H % Hkv == 0, query head h reads
+ * kv head h / (H/Hkv)).  Writes out ([B,H,T,D], any strides as above) and
+ * lse ([B,H,T] fp32 contiguous; +inf marks a row with no valid source).
+ * Scale is head_dim**-0.5 in fp32.
+ */
+int sbda_forward(const void* q, const int64_t* q_strides,
+                 const void* k, const int64_t* k_strides,
+                 const void* v, const int64_t* v_strides,
+                 void* out, const int64_t* out_strides,
+                 float* lse,
+                 int64_t batch, int64_t heads, int64_t kv_heads,
+                 int64_t length, int64_t head_dim, int32_t dtype,
+                 const int32_t* offsets, int32_t num_offsets,
+                 void* stream);
+
+/*
+ * Backward from the forward's saved q, k, v and lse.  Writes dq, dk, dv (each
+ * row exactly once: deterministic, no atomics).
+ */
+int sbda_backward(const void* q, const int64_t* q_strides,
+                  const void* k, const int64_t* k_strides,
+                  const void* v, const int64_t* v_strides,
+                  const void* dout, const int64_t* dout_strides,
+                  const float* lse,
+                  void* dq, const int64_t* dq_strides,
+                  void* dk, const int64_t* dk_strides,
+                  void* dv, const int64_t* dv_strides,
+                  int64_t batch, int64_t heads, int64_t kv_heads,
+                  int64_t length, int64_t head_dim, int32_t dtype,
+                  const int32_t* offsets, int32_t num_offsets,
+                  void* stream);
+
+/*
+ * Forward with the head-RMSNorm + RoPE prologue fused: q_raw and k_raw are
+ * the projections before normalisation; q_weight/k_weight are fp32 [D]
+ * norm weights; rope_cos/rope_sin are [T, D/2] tables in the activation
+ * dtype (sbda_rope_table).  eps is the norm epsilon (reference: 1e-6).
+ */
+int sbda_forward_prologue(const void* q_raw, const int64_t* q_strides,
+                          const void* k_raw, const int64_t* k_strides,
+                          const void* v, const int64_t* v_strides,
+                          void* out, const int64_t* out_strides,
+                          float* lse,
+                          const float* q_weight, const float* k_weight,
+                          const void* rope_cos, const void* rope_sin, float eps,
+                          int64_t batch, int64_t heads, int64_t kv_heads,
+                          int64_t length, int64_t head_dim, int32_t dtype,
+                          const int32_t* offsets, int32_t num_offsets,
+                          void* stream);
+
+/* Workspace bytes sbda_backward_prologue needs for these shapes (< 0: error). */
+int64_t sbda_backward_prologue_workspace(int64_t batch, int64_t heads, int64_t kv_heads,
+                                         int64_t length, int64_t head_dim, int32_t dtype,
+                                         const int32_t* offsets, int32_t num_offsets);
+
+/*
+ * Backward of sbda_forward_prologue: gradients of the raw q/k, of v and of
+ * the two norm weights (dq_weight, dk_weight: fp32 [D], overwritten; summed
+ * over all rows in a fixed order through `workspace`).
+ */
+int sbda_backward_prologue(const void* q_raw, const int64_t* q_strides,
+                           const void* k_raw, const int64_t* k_strides,
+                           const void* v, const int64_t* v_strides,
+                           const void* dout, const int64_t* dout_strides,
+                           const float* lse,
+                           const float* q_weight, const float* k_weight,
+                           const void* rope_cos, const void* rope_sin, float eps,
+                           void* dq_raw, const int64_t* dq_strides,
+                           void* dk_raw, const int64_t* dk_strides,
+                           void* dv, const int64_t* dv_strides,
+                           float* dq_weight, float* dk_weight,
+                           void* workspace, int64_t workspace_bytes,
+                           int64_t batch, int64_t heads, int64_t kv_heads,
+                           int64_t length, int64_t head_dim, int32_t dtype,
+                           const int32_t* offsets, int32_t num_offsets,
+                           void* stream);
+
+/*
+ * RoPE tables: cos/sin[t, i] = cos/sin(fl32(t * inv_freq[i])) for t < length,
+ * i < head_dim/2, stored in `dtype`.  inv_freq is a host fp32 array of
+ * head_dim/2 values (head_dim <= 512).
+ */
+int sbda_rope_table(void* rope_cos, void* rope_sin, const float* inv_freq,
+                    int64_t length, int64_t head_dim, int32_t dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SBDA_AMD_H */

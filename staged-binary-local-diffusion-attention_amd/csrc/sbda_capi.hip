@@ -1,0 +1,276 @@
+// C ABI (include/sbda_amd.h): argument validation, parameter packing and
+// dispatch to the kernels.  No device allocation happens here.
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "sbda_amd.h"
+#include "sbda_params.h"
+
+namespace sbda {
+
+hipError_t direct_forward(const Params& p, int dtype, bool pro, hipStream_t st);
+hipError_t direct_backward(const Params& p, int dtype, bool pro, hipStream_t st);
+void direct_partials(const Params& p, int esz, int64_t* parts_q, int64_t* parts_k);
+bool walk_applies(const Params& p, int dtype);
+hipError_t walk_forward(const Params& p, int dtype, bool pro, hipStream_t st);
+hipError_t walk_backward(const Params& p, int dtype, bool pro, hipStream_t st);
+void walk_partials(const Params& p, int dtype, int64_t* parts_q, int64_t* parts_k);
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int esize(int dtype) { return dtype == kFP32 ? 4 : 2; }
+
+// Shapes, dtype and offsets shared by every entry point.
+int check_problem(int64_t batch, int64_t heads, int64_t kv_heads, int64_t length,
+                  int64_t head_dim, int32_t dtype, const int32_t* offsets,
+                  int32_t num_offsets, Params& p) {
+  if (dtype != kBF16 && dtype != kFP16 && dtype != kFP32)
+    return fail(SBDA_ERR_DTYPE, "unsupported SBDA dtype code %d (bf16, fp16 or fp32)", (int)dtype);
+  if (batch <= 0 || heads <= 0 || kv_heads <= 0 || length <= 0 || head_dim <= 0)
+    return fail(SBDA_ERR_VALUE, "SBDA sizes must be positive (B=%lld H=%lld Hkv=%lld T=%lld D=%lld)",
+                (long long)batch, (long long)heads, (long long)kv_heads, (long long)length,
+                (long long)head_dim);
+  if (heads % kv_heads)
+    return fail(SBDA_ERR_VALUE, "query heads (%lld) must be divisible by kv heads (%lld)",
+                (long long)heads, (long long)kv_heads);
+  if (length >= (int64_t(1) << 31) - 1 || batch >= (int64_t(1) << 31) || heads >= (1 << 20))
+    return fail(SBDA_ERR_VALUE, "SBDA sizes exceed the supported range");
+  const int esz = esize(dtype);
+  if ((head_dim * esz) % 16 != 0 || head_dim * esz > 512)
+    return fail(SBDA_ERR_VALUE,
+                "head_dim %lld unsupported: head_dim * element size must be a multiple of 16 bytes "
+                "and at most 512 bytes",
+                (long long)head_dim);
+  if (offsets == nullptr || num_offsets < 1 || num_offsets > kMaxSlots)
+    return fail(SBDA_ERR_VALUE, "SBDA supports 1 to %d sources, got %d", kMaxSlots, (int)num_offsets);
+  std::memset(&p, 0, sizeof(p));
+  for (int s = 0; s < num_offsets; ++s) {
+    if (offsets[s] < 0) return fail(SBDA_ERR_VALUE, "SBDA offsets must be >= 0 (slot %d is %d)", s, offsets[s]);
+    p.off[s] = offsets[s];
+  }
+  p.B = (int)batch;
+  p.H = (int)heads;
+  p.Hkv = (int)kv_heads;
+  p.group = (int)(heads / kv_heads);
+  p.T = (int)length;
+  p.D = (int)head_dim;
+  p.S = num_offsets;
+  p.scale = (float)(1.0 / __builtin_sqrt((double)head_dim));
+  return SBDA_OK;
+}
+
+int check_view(const char* name, const void* ptr, const int64_t* strides, int esz, bool writable,
+               View* out) {
+  if (ptr == nullptr || strides == nullptr) return fail(SBDA_ERR_VALUE, "%s: null pointer", name);
+  if (reinterpret_cast<uintptr_t>(ptr) % 16)
+    return fail(SBDA_ERR_VALUE, "%s: data pointer must be 16-byte aligned", name);
+  if (strides[3] != 1) return fail(SBDA_ERR_VALUE, "%s: head_dim stride must be 1", name);
+  for (int i = 0; i < 3; ++i)
+    if ((strides[i] * esz) % 16)
+      return fail(SBDA_ERR_VALUE, "%s: stride %d must be a multiple of 16 bytes", name, i);
+  (void)writable;
+  out->p = ptr;
+  out->sb = strides[0];
+  out->sh = strides[1];
+  out->st = strides[2];
+  return SBDA_OK;
+}
+
+int check_mut(const char* name, void* ptr, const int64_t* strides, int esz, MutView* out) {
+  View v;
+  int rc = check_view(name, ptr, strides, esz, true, &v);
+  if (rc) return rc;
+  out->p = ptr;
+  out->sb = v.sb;
+  out->sh = v.sh;
+  out->st = v.st;
+  return SBDA_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return SBDA_OK;
+  return fail(SBDA_ERR_RUNTIME, "%s: HIP error %d (%s)", what, (int)e, hipGetErrorString(e));
+}
+
+int forward_impl(bool pro, const void* q, const int64_t* qs, const void* k, const int64_t* ks,
+                 const void* v, const int64_t* vs, void* out, const int64_t* os, float* lse,
+                 const float* wq, const float* wk, const void* rc, const void* rs, float eps,
+                 int64_t batch, int64_t heads, int64_t kv_heads, int64_t length, int64_t head_dim,
+                 int32_t dtype, const int32_t* offsets, int32_t n, void* stream) {
+  g_error.clear();
+  Params p;
+  int rc_ = check_problem(batch, heads, kv_heads, length, head_dim, dtype, offsets, n, p);
+  if (rc_) return rc_;
+  const int esz = esize(dtype);
+  if ((rc_ = check_view("q", q, qs, esz, false, &p.q))) return rc_;
+  if ((rc_ = check_view("k", k, ks, esz, false, &p.k))) return rc_;
+  if ((rc_ = check_view("v", v, vs, esz, false, &p.v))) return rc_;
+  if ((rc_ = check_mut("out", out, os, esz, &p.o))) return rc_;
+  if (lse == nullptr) return fail(SBDA_ERR_VALUE, "lse: null pointer");
+  p.lse = lse;
+  if (pro) {
+    if (!wq || !wk || !rc || !rs) return fail(SBDA_ERR_VALUE, "prologue: null weight or RoPE table");
+    p.wq = wq;
+    p.wk = wk;
+    p.rope_cos = rc;
+    p.rope_sin = rs;
+    p.eps = eps;
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e = walk_applies(p, dtype) ? walk_forward(p, dtype, pro, st)
+                                        : direct_forward(p, dtype, pro, st);
+  return hip_status(e, "sbda forward launch");
+}
+
+void partials(const Params& p, int dtype, int64_t* pq, int64_t* pk) {
+  if (walk_applies(p, dtype))
+    walk_partials(p, dtype, pq, pk);
+  else
+    direct_partials(p, esize(dtype), pq, pk);
+}
+
+int backward_impl(bool pro, const void* q, const int64_t* qs, const void* k, const int64_t* ks,
+                  const void* v, const int64_t* vs, const void* dout, const int64_t* dos,
+                  const float* lse, const float* wq, const float* wk, const void* rc,
+                  const void* rs, float eps, void* dq, const int64_t* dqs, void* dk,
+                  const int64_t* dks, void* dv, const int64_t* dvs, float* dwq, float* dwk,
+                  void* ws, int64_t ws_bytes, int64_t batch, int64_t heads, int64_t kv_heads,
+                  int64_t length, int64_t head_dim, int32_t dtype, const int32_t* offsets,
+                  int32_t n, void* stream) {
+  g_error.clear();
+  Params p;
+  int rc_ = check_problem(batch, heads, kv_heads, length, head_dim, dtype, offsets, n, p);
+  if (rc_) return rc_;
+  const int esz = esize(dtype);
+  if ((rc_ = check_view("q", q, qs, esz, false, &p.q))) return rc_;
+  if ((rc_ = check_view("k", k, ks, esz, false, &p.k))) return rc_;
+  if ((rc_ = check_view("v", v, vs, esz, false, &p.v))) return rc_;
+  if ((rc_ = check_view("grad_out", dout, dos, esz, false, &p.dout))) return rc_;
+  if ((rc_ = check_mut("dq", dq, dqs, esz, &p.dq))) return rc_;
+  if ((rc_ = check_mut("dk", dk, dks, esz, &p.dk))) return rc_;
+  if ((rc_ = check_mut("dv", dv, dvs, esz, &p.dv))) return rc_;
+  if (lse == nullptr) return fail(SBDA_ERR_VALUE, "lse: null pointer");
+  p.lse = const_cast<float*>(lse);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  int64_t pq = 0, pk = 0;
+  if (pro) {
+    if (!wq || !wk || !rc || !rs || !dwq || !dwk)
+      return fail(SBDA_ERR_VALUE, "prologue: null weight, weight-gradient or RoPE table");
+    partials(p, dtype, &pq, &pk);
+    const int64_t need = (pq + pk) * p.D * (int64_t)sizeof(float);
+    if (ws == nullptr || ws_bytes < need)
+      return fail(SBDA_ERR_VALUE, "prologue backward: workspace of %lld bytes needed, %lld given",
+                  (long long)need, (long long)ws_bytes);
+    if (reinterpret_cast<uintptr_t>(ws) % 16) return fail(SBDA_ERR_VALUE, "workspace must be 16-byte aligned");
+    p.wq = wq;
+    p.wk = wk;
+    p.rope_cos = rc;
+    p.rope_sin = rs;
+    p.eps = eps;
+    p.dwq_part = reinterpret_cast<float*>(ws);
+    p.dwk_part = p.dwq_part + pq * p.D;
+  }
+  hipError_t e = walk_applies(p, dtype) ? walk_backward(p, dtype, pro, st)
+                                        : direct_backward(p, dtype, pro, st);
+  if (e == hipSuccess && pro) {
+    e = launch_reduce_partials(p.dwq_part, pq, p.D, dwq, st);
+    if (e == hipSuccess) e = launch_reduce_partials(p.dwk_part, pk, p.D, dwk, st);
+  }
+  return hip_status(e, "sbda backward launch");
+}
+
+}  // namespace
+}  // namespace sbda
+
+using namespace sbda;
+
+extern "C" {
+
+int sbda_abi_version(void) { return 1; }
+
+const char* sbda_last_error(void) { return g_error.c_str(); }
+
+int sbda_forward(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
+                 const int64_t* vs, void* out, const int64_t* os, float* lse, int64_t batch,
+                 int64_t heads, int64_t kv_heads, int64_t length, int64_t head_dim, int32_t dtype,
+                 const int32_t* offsets, int32_t n, void* stream) {
+  return forward_impl(false, q, qs, k, ks, v, vs, out, os, lse, nullptr, nullptr, nullptr, nullptr,
+                      0.f, batch, heads, kv_heads, length, head_dim, dtype, offsets, n, stream);
+}
+
+int sbda_backward(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
+                  const int64_t* vs, const void* dout, const int64_t* dos, const float* lse, void* dq,
+                  const int64_t* dqs, void* dk, const int64_t* dks, void* dv, const int64_t* dvs,
+                  int64_t batch, int64_t heads, int64_t kv_heads, int64_t length, int64_t head_dim,
+                  int32_t dtype, const int32_t* offsets, int32_t n, void* stream) {
+  return backward_impl(false, q, qs, k, ks, v, vs, dout, dos, lse, nullptr, nullptr, nullptr, nullptr,
+                       0.f, dq, dqs, dk, dks, dv, dvs, nullptr, nullptr, nullptr, 0, batch, heads,
+                       kv_heads, length, head_dim, dtype, offsets, n, stream);
+}
+
+int sbda_forward_prologue(const void* q, const int64_t* qs, const void* k, const int64_t* ks,
+                          const void* v, const int64_t* vs, void* out, const int64_t* os,
+                          float* lse, const float* wq, const float* wk, const void* rc,
+                          const void* rs, float eps, int64_t batch, int64_t heads,
+                          int64_t kv_heads, int64_t length, int64_t head_dim, int32_t dtype,
+                          const int32_t* offsets, int32_t n, void* stream) {
+  return forward_impl(true, q, qs, k, ks, v, vs, out, os, lse, wq, wk, rc, rs, eps, batch, heads,
+                      kv_heads, length, head_dim, dtype, offsets, n, stream);
+}
+
+int64_t sbda_backward_prologue_workspace(int64_t batch, int64_t heads, int64_t kv_heads,
+                                         int64_t length, int64_t head_dim, int32_t dtype,
+                                         const int32_t* offsets, int32_t n) {
+  g_error.clear();
+  Params p;
+  int rc = check_problem(batch, heads, kv_heads, length, head_dim, dtype, offsets, n, p);
+  if (rc) return -rc;
+  int64_t pq = 0, pk = 0;
+  partials(p, dtype, &pq, &pk);
+  return (pq + pk) * p.D * (int64_t)sizeof(float);
+}
+
+int sbda_backward_prologue(const void* q, const int64_t* qs, const void* k, const int64_t* ks,
+                           const void* v, const int64_t* vs, const void* dout, const int64_t* dos,
+                           const float* lse, const float* wq, const float* wk, const void* rc,
+                           const void* rs, float eps, void* dq, const int64_t* dqs, void* dk,
+                           const int64_t* dks, void* dv, const int64_t* dvs, float* dwq,
+                           float* dwk, void* ws, int64_t ws_bytes, int64_t batch, int64_t heads,
+                           int64_t kv_heads, int64_t length, int64_t head_dim, int32_t dtype,
+                           const int32_t* offsets, int32_t n, void* stream) {
+  return backward_impl(true, q, qs, k, ks, v, vs, dout, dos, lse, wq, wk, rc, rs, eps, dq, dqs, dk,
+                       dks, dv, dvs, dwq, dwk, ws, ws_bytes, batch, heads, kv_heads, length, head_dim,
+                       dtype, offsets, n, stream);
+}
+
+int sbda_rope_table(void* rope_cos, void* rope_sin, const float* inv_freq, int64_t length,
+                    int64_t head_dim, int32_t dtype, void* stream) {
+  g_error.clear();
+  if (dtype != kBF16 && dtype != kFP16 && dtype != kFP32)
+    return fail(SBDA_ERR_DTYPE, "unsupported RoPE table dtype code %d", (int)dtype);
+  if (!rope_cos || !rope_sin || !inv_freq) return fail(SBDA_ERR_VALUE, "RoPE table: null pointer");
+  if (length <= 0 || head_dim <= 0 || head_dim % 2 || head_dim > 512)
+    return fail(SBDA_ERR_VALUE, "RoPE table: bad length %lld or head_dim %lld", (long long)length,
+                (long long)head_dim);
+  hipError_t e = launch_rope_table(rope_cos, rope_sin, inv_freq, length, (int)(head_dim / 2), dtype,
+                                   reinterpret_cast<hipStream_t>(stream));
+  return hip_status(e, "sbda rope table launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,457 @@
+// Row-parallel SBDA kernels for every supported shape.
+//
+// One lane group (LPR lanes) owns one row and reads each of its sources
+// straight from global memory; neighbouring rows' re-reads are served by the
+// caches.  These kernels accept any batch/head/GQA/head_dim/stride/offset
+// combination the C ABI validates.  The wavefront-walk kernels in
+// sbda_walk.hip are used instead where their layout applies.
+//
+// Maths (per batch b, query head h, kv head hk = h / group, query row i,
+// slot s with source j = i - off[s], valid iff j >= 0; reference
+// BiAttn/left_v2.py:313-405 and BiAttn/sbda_triton.py:135-201,507-671):
+//   score_s = (q_i . k_j) * scale,     p = softmax over valid slots,
+//   o_i = sum_s p_s v_j,               lse_i = log sum_valid exp(score_s),
+//   dP_s = dO_i . v_j,  delta_i = sum_s p_s dP_s,  dS_s = p_s (dP_s - delta_i),
+//   dQ_i = scale sum_s dS_s k_j,
+//   dK_j = scale sum_{h in group} sum_t dS_t(i = j + off[t]) q_i   (i < T),
+//   dV_j =       sum_{h in group} sum_t p_t(i = j + off[t]) dO_i.
+// A row with no valid source has o = 0, gradient 0 and lse = +inf.
+
+#include <type_traits>
+
+#include "sbda_device.h"
+#include "sbda_params.h"
+
+namespace sbda {
+
+constexpr int kBlock = 256;
+
+template <typename T>
+__device__ inline const T* row_ptr(const View& v, int b, int h, int64_t t) {
+  return reinterpret_cast<const T*>(v.p) + (int64_t)b * v.sb + (int64_t)h * v.sh + t * v.st;
+}
+template <typename T>
+__device__ inline T* row_ptr(const MutView& v, int b, int h, int64_t t) {
+  return reinterpret_cast<T*>(v.p) + (int64_t)b * v.sb + (int64_t)h * v.sh + t * v.st;
+}
+
+// Loads k (through the prologue when fused) of source row `t` for kv head hk.
+template <typename T, int LPR, bool PRO>
+__device__ inline void load_key(const Params& p, int b, int hk, int64_t t, int li,
+                                float (&k)[VecOf<T>::value]) {
+  load_row<T, PRO>(row_ptr<T>(p.k, b, hk, t), li, p.D, k);
+  if constexpr (PRO) {
+    using PL = Prologue<T, LPR>;
+    float c[PL::HV], s[PL::HV];
+    PL::load_cs((const T*)p.rope_cos, (const T*)p.rope_sin, t, li, p.D, c, s);
+    PL::forward(k, p.wk, c, s, li, p.D, p.eps);
+  }
+}
+
+// Decodes a global row id into (b, t, h) with heads fastest.
+__device__ inline void decode_row(int64_t row, int heads, int T, int& b, int& t, int& h) {
+  h = (int)(row % heads);
+  const int64_t bt = row / heads;
+  t = (int)(bt % T);
+  b = (int)(bt / T);
+}
+
+// Deterministic block reduction of per-lane weight-gradient registers into
+// out[d] (d < D): lane groups are summed in increasing order.
+template <typename T, int LPR, bool SPLIT>
+__device__ inline void block_reduce_dw(const float (&dw)[VecOf<T>::value], int D, float* out) {
+  constexpr int VEC = VecOf<T>::value;
+  constexpr int HV = VEC / 2;
+  __shared__ float buf[kBlock * VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) buf[threadIdx.x * VEC + i] = dw[i];
+  __syncthreads();
+  const int groups = kBlock / LPR;
+  for (int d = threadIdx.x; d < D; d += kBlock) {
+    int li, slot;
+    if constexpr (SPLIT) {
+      const int half = D >> 1;
+      const int dd = d < half ? d : d - half;
+      li = dd / HV;
+      slot = (dd % HV) + (d < half ? 0 : HV);
+    } else {
+      li = d / VEC;
+      slot = d % VEC;
+    }
+    float acc = 0.f;
+    for (int g = 0; g < groups; ++g) acc += buf[(g * LPR + li) * VEC + slot];
+    out[d] = acc;
+  }
+}
+
+// ----------------------------------------------------------------- forward
+
+template <typename T, int LPR, bool PRO>
+__global__ __launch_bounds__(kBlock) void fwd_direct(Params p) {
+  constexpr int VEC = VecOf<T>::value;
+  const int li = threadIdx.x % LPR;
+  const int64_t nrows = (int64_t)p.B * p.T * p.H;
+  int64_t row = ((int64_t)blockIdx.x * kBlock + threadIdx.x) / LPR;
+  const bool live = row < nrows;
+  if (!live) row = 0;  // keep every lane in the row reductions
+  int b, t, h;
+  decode_row(row, p.H, p.T, b, t, h);
+  const int hk = h / p.group;
+
+  float q[VEC];
+  load_row<T, PRO>(row_ptr<T>(p.q, b, h, t), li, p.D, q);
+  if constexpr (PRO) {
+    using PL = Prologue<T, LPR>;
+    float c[PL::HV], s[PL::HV];
+    PL::load_cs((const T*)p.rope_cos, (const T*)p.rope_sin, t, li, p.D, c, s);
+    PL::forward(q, p.wq, c, s, li, p.D, p.eps);
+  }
+
+  float sc[kMaxSlots];
+  int src[kMaxSlots];
+  float m = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < kMaxSlots; ++s) {
+    if (s < p.S) {
+      const int j = t - p.off[s];
+      src[s] = j;
+      float k[VEC];
+      load_key<T, LPR, PRO>(p, b, hk, j >= 0 ? j : 0, li, k);
+      const float d = row_sum<LPR>(dot_partial<VEC>(q, k)) * p.scale;
+      sc[s] = j >= 0 ? d : -INFINITY;
+      m = fmaxf(m, sc[s]);
+    }
+  }
+  float acc[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) acc[i] = 0.f;
+  float l = 0.f;
+#pragma unroll
+  for (int s = 0; s < kMaxSlots; ++s) {
+    if (s < p.S) {
+      const int j = src[s];
+      const float w = j >= 0 ? fast_exp(sc[s] - m) : 0.f;
+      l += w;
+      float v[VEC];
+      load_row<T, PRO>(row_ptr<T>(p.v, b, hk, j >= 0 ? j : 0), li, p.D, v);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) acc[i] = __builtin_fmaf(w, v[i], acc[i]);
+    }
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) acc[i] *= inv;
+  if (live) {
+    store_row<T, PRO>(row_ptr<T>(p.o, b, h, t), li, p.D, acc);
+    if (li == 0) p.lse[((int64_t)b * p.H + h) * p.T + t] = l > 0.f ? m + fast_log(l) : INFINITY;
+  }
+}
+
+// -------------------------------------------------------------- query side
+//
+// Recomputes, for query row (b, i, h): its (roped) q, dO, per-slot weights
+// p_s and score gradients dS_s.  Keys of the sources are returned in `kk`
+// when WANT_K (for dQ).
+template <typename T, int LPR, bool PRO, bool WANT_K>
+__device__ inline void query_side(const Params& p, int b, int i, int h, int hk, int li,
+                                  float (&q)[VecOf<T>::value], float (&go)[VecOf<T>::value],
+                                  float (&pp)[kMaxSlots], float (&ds)[kMaxSlots],
+                                  float (&kk)[kMaxSlots][VecOf<T>::value]) {
+  constexpr int VEC = VecOf<T>::value;
+  load_row<T, PRO>(row_ptr<T>(p.q, b, h, i), li, p.D, q);
+  if constexpr (PRO) {
+    using PL = Prologue<T, LPR>;
+    float c[PL::HV], s[PL::HV];
+    PL::load_cs((const T*)p.rope_cos, (const T*)p.rope_sin, i, li, p.D, c, s);
+    PL::forward(q, p.wq, c, s, li, p.D, p.eps);
+  }
+  load_row<T, PRO>(row_ptr<T>(p.dout, b, h, i), li, p.D, go);
+  const float lse = p.lse[((int64_t)b * p.H + h) * p.T + i];
+  float dp[kMaxSlots];
+  float delta = 0.f;
+#pragma unroll
+  for (int s = 0; s < kMaxSlots; ++s) {
+    pp[s] = 0.f;
+    dp[s] = 0.f;
+    if (s < p.S) {
+      const int j = i - p.off[s];
+      const int jc = j >= 0 ? j : 0;
+      float k[VEC], v[VEC];
+      load_key<T, LPR, PRO>(p, b, hk, jc, li, k);
+      load_row<T, PRO>(row_ptr<T>(p.v, b, hk, jc), li, p.D, v);
+      const float sc = row_sum<LPR>(dot_partial<VEC>(q, k)) * p.scale;
+      const float d = row_sum<LPR>(dot_partial<VEC>(go, v));
+      pp[s] = j >= 0 ? fast_exp(sc - lse) : 0.f;  // lse = +inf -> 0
+      dp[s] = d;
+      delta = __builtin_fmaf(pp[s], d, delta);
+      if constexpr (WANT_K) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) kk[s][e] = k[e];
+      }
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < kMaxSlots; ++s) ds[s] = pp[s] * (dp[s] - delta);
+}
+
+// ------------------------------------------------------------ backward: dQ
+
+template <typename T, int LPR, bool PRO>
+__global__ __launch_bounds__(kBlock) void bwd_dq_direct(Params p) {
+  constexpr int VEC = VecOf<T>::value;
+  const int li = threadIdx.x % LPR;
+  const int64_t nrows = (int64_t)p.B * p.T * p.H;
+  int64_t row = ((int64_t)blockIdx.x * kBlock + threadIdx.x) / LPR;
+  const bool live = row < nrows;
+  if (!live) row = 0;
+  int b, t, h;
+  decode_row(row, p.H, p.T, b, t, h);
+  const int hk = h / p.group;
+
+  float q[VEC], go[VEC], pp[kMaxSlots], ds[kMaxSlots], kk[kMaxSlots][VEC];
+  query_side<T, LPR, PRO, true>(p, b, t, h, hk, li, q, go, pp, ds, kk);
+  float dq[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    float a = 0.f;
+#pragma unroll
+    for (int s = 0; s < kMaxSlots; ++s)
+      if (s < p.S) a = __builtin_fmaf(ds[s], kk[s][e], a);
+    dq[e] = a * p.scale;
+  }
+  if constexpr (PRO) {
+    using PL = Prologue<T, LPR>;
+    float x[VEC], c[PL::HV], s[PL::HV], dw[VEC];
+    load_row<T, true>(row_ptr<T>(p.q, b, h, t), li, p.D, x);
+    PL::load_cs((const T*)p.rope_cos, (const T*)p.rope_sin, t, li, p.D, c, s);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) ss = __builtin_fmaf(x[e], x[e], ss);
+    ss = row_sum<LPR>(ss);
+    const float r = __builtin_amdgcn_rsqf(__fadd_rn(__fdiv_rn(ss, (float)p.D), p.eps));
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) dw[e] = 0.f;
+    PL::backward(dq, x, r, p.wq, c, s, li, p.D, dw);
+    if (!live) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) dw[e] = 0.f;
+    }
+    block_reduce_dw<T, LPR, true>(dw, p.D, p.dwq_part + (int64_t)blockIdx.x * p.D);
+  }
+  if (live) store_row<T, PRO>(row_ptr<T>(p.dq, b, h, t), li, p.D, dq);
+}
+
+// ---------------------------------------------------------- backward: dK dV
+
+template <typename T, int LPR, bool PRO>
+__global__ __launch_bounds__(kBlock) void bwd_dkv_direct(Params p) {
+  constexpr int VEC = VecOf<T>::value;
+  const int li = threadIdx.x % LPR;
+  const int64_t nrows = (int64_t)p.B * p.T * p.Hkv;
+  int64_t row = ((int64_t)blockIdx.x * kBlock + threadIdx.x) / LPR;
+  const bool live = row < nrows;
+  if (!live) row = 0;
+  int b, j, hk;
+  decode_row(row, p.Hkv, p.T, b, j, hk);
+
+  float dk[VEC], dv[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) { dk[e] = 0.f; dv[e] = 0.f; }
+  for (int g = 0; g < p.group; ++g) {
+    const int h = hk * p.group + g;
+#pragma unroll
+    for (int tslot = 0; tslot < kMaxSlots; ++tslot) {
+      if (tslot < p.S) {
+        const int64_t i64 = (int64_t)j + p.off[tslot];
+        const bool ok = i64 < p.T;
+        const int i = ok ? (int)i64 : j;
+        float q[VEC], go[VEC], pp[kMaxSlots], ds[kMaxSlots], kk[kMaxSlots][VEC];
+        query_side<T, LPR, PRO, false>(p, b, i, h, hk, li, q, go, pp, ds, kk);
+        float pt = 0.f, dst = 0.f;
+#pragma unroll
+        for (int s = 0; s < kMaxSlots; ++s)
+          if (s == tslot) { pt = pp[s]; dst = ds[s]; }
+        if (!ok) { pt = 0.f; dst = 0.f; }
+        dst *= p.scale;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          dk[e] = __builtin_fmaf(dst, q[e], dk[e]);
+          dv[e] = __builtin_fmaf(pt, go[e], dv[e]);
+        }
+      }
+    }
+  }
+  if constexpr (PRO) {
+    using PL = Prologue<T, LPR>;
+    float x[VEC], c[PL::HV], s[PL::HV], dw[VEC];
+    load_row<T, true>(row_ptr<T>(p.k, b, hk, j), li, p.D, x);
+    PL::load_cs((const T*)p.rope_cos, (const T*)p.rope_sin, j, li, p.D, c, s);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) ss = __builtin_fmaf(x[e], x[e], ss);
+    ss = row_sum<LPR>(ss);
+    const float r = __builtin_amdgcn_rsqf(__fadd_rn(__fdiv_rn(ss, (float)p.D), p.eps));
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) dw[e] = 0.f;
+    PL::backward(dk, x, r, p.wk, c, s, li, p.D, dw);
+    if (!live) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) dw[e] = 0.f;
+    }
+    block_reduce_dw<T, LPR, true>(dw, p.D, p.dwk_part + (int64_t)blockIdx.x * p.D);
+  }
+  if (live) {
+    store_row<T, PRO>(row_ptr<T>(p.dk, b, hk, j), li, p.D, dk);
+    store_row<T, PRO>(row_ptr<T>(p.dv, b, hk, j), li, p.D, dv);
+  }
+}
+
+// ------------------------------------------------------------ dispatchers
+
+template <typename T, bool PRO>
+struct DirectLaunch {
+  template <int LPR>
+  static hipError_t fwd(const Params& p, hipStream_t st) {
+    const int64_t rows = (int64_t)p.B * p.T * p.H;
+    const int64_t blocks = (rows * LPR + kBlock - 1) / kBlock;
+    hipLaunchKernelGGL((fwd_direct<T, LPR, PRO>), dim3((unsigned)blocks), dim3(kBlock), 0, st, p);
+    return hipGetLastError();
+  }
+  template <int LPR>
+  static hipError_t bwd(const Params& p, hipStream_t st) {
+    const int64_t qrows = (int64_t)p.B * p.T * p.H;
+    const int64_t krows = (int64_t)p.B * p.T * p.Hkv;
+    const int64_t qb = (qrows * LPR + kBlock - 1) / kBlock;
+    const int64_t kb = (krows * LPR + kBlock - 1) / kBlock;
+    hipLaunchKernelGGL((bwd_dq_direct<T, LPR, PRO>), dim3((unsigned)qb), dim3(kBlock), 0, st, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((bwd_dkv_direct<T, LPR, PRO>), dim3((unsigned)kb), dim3(kBlock), 0, st, p);
+    return hipGetLastError();
+  }
+};
+
+template <typename F>
+static hipError_t by_lpr(int lpr, F&& f) {
+  switch (lpr) {
+    case 1: return f(std::integral_constant<int, 1>{});
+    case 2: return f(std::integral_constant<int, 2>{});
+    case 4: return f(std::integral_constant<int, 4>{});
+    case 8: return f(std::integral_constant<int, 8>{});
+    case 16: return f(std::integral_constant<int, 16>{});
+    case 32: return f(std::integral_constant<int, 32>{});
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <typename T, bool PRO>
+static hipError_t direct_forward_t(const Params& p, hipStream_t st) {
+  const int lpr = lanes_per_row(p.D, sizeof(T));
+  return by_lpr(lpr, [&](auto c) { return DirectLaunch<T, PRO>::template fwd<decltype(c)::value>(p, st); });
+}
+
+template <typename T, bool PRO>
+static hipError_t direct_backward_t(const Params& p, hipStream_t st) {
+  const int lpr = lanes_per_row(p.D, sizeof(T));
+  return by_lpr(lpr, [&](auto c) { return DirectLaunch<T, PRO>::template bwd<decltype(c)::value>(p, st); });
+}
+
+hipError_t direct_forward(const Params& p, int dtype, bool pro, hipStream_t st) {
+  switch (dtype) {
+    case kBF16: return pro ? direct_forward_t<__bf16, true>(p, st) : direct_forward_t<__bf16, false>(p, st);
+    case kFP16: return pro ? direct_forward_t<_Float16, true>(p, st) : direct_forward_t<_Float16, false>(p, st);
+    case kFP32: return pro ? direct_forward_t<float, true>(p, st) : direct_forward_t<float, false>(p, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t direct_backward(const Params& p, int dtype, bool pro, hipStream_t st) {
+  switch (dtype) {
+    case kBF16: return pro ? direct_backward_t<__bf16, true>(p, st) : direct_backward_t<__bf16, false>(p, st);
+    case kFP16: return pro ? direct_backward_t<_Float16, true>(p, st) : direct_backward_t<_Float16, false>(p, st);
+    case kFP32: return pro ? direct_backward_t<float, true>(p, st) : direct_backward_t<float, false>(p, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+void direct_partials(const Params& p, int esz, int64_t* parts_q, int64_t* parts_k) {
+  const int lpr = lanes_per_row(p.D, esz);
+  const int64_t qrows = (int64_t)p.B * p.T * p.H;
+  const int64_t krows = (int64_t)p.B * p.T * p.Hkv;
+  *parts_q = (qrows * lpr + kBlock - 1) / kBlock;
+  *parts_k = (krows * lpr + kBlock - 1) / kBlock;
+}
+
+// ------------------------------------------------------- partial reduction
+
+constexpr int kReduceBlock = 256;
+
+__global__ __launch_bounds__(kReduceBlock) void reduce_partials_kernel(const float* __restrict__ part,
+                                                                       int64_t parts, int D,
+                                                                       float* __restrict__ out) {
+  __shared__ float buf[kReduceBlock];
+  const int d = blockIdx.x;
+  float acc = 0.f;
+  for (int64_t k = threadIdx.x; k < parts; k += kReduceBlock) acc += part[k * D + d];
+  buf[threadIdx.x] = acc;
+  __syncthreads();
+  for (int w = kReduceBlock / 2; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) buf[threadIdx.x] += buf[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[d] = buf[0];
+}
+
+hipError_t launch_reduce_partials(const float* part, int64_t parts, int D, float* out, hipStream_t st) {
+  hipLaunchKernelGGL(reduce_partials_kernel, dim3((unsigned)D), dim3(kReduceBlock), 0, st, part, parts, D, out);
+  return hipGetLastError();
+}
+
+// --------------------------------------------------------------- RoPE table
+//
+// cos/sin[t, i] = cos/sin(fl32(t * inv_freq[i])) cast to the activation
+// dtype: the reference builds angles as an fp32 outer product
+// (BiAttn/attention_common.py:18-21).  inv_freq is computed on the host with
+// the reference's own fp32 expression so the angles agree bit for bit.
+struct InvFreq {
+  float v[256];
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void rope_table_kernel(T* __restrict__ cos_out, T* __restrict__ sin_out,
+                                                         InvFreq f, int64_t T_, int half) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= T_ * half) return;
+  const int64_t t = idx / half;
+  const int i = (int)(idx % half);
+  const float ang = __fmul_rn((float)t, f.v[i]);
+  float s, c;
+  sincosf(ang, &s, &c);
+  cos_out[idx] = (T)c;
+  sin_out[idx] = (T)s;
+}
+
+hipError_t launch_rope_table(void* cos_out, void* sin_out, const float* inv_freq_host,
+                             int64_t T_, int half, int dtype, hipStream_t st) {
+  if (half > 256) return hipErrorInvalidValue;
+  InvFreq f;
+  for (int i = 0; i < 256; ++i) f.v[i] = i < half ? inv_freq_host[i] : 0.f;
+  const int64_t n = T_ * half;
+  const dim3 grid((unsigned)((n + 255) / 256));
+  switch (dtype) {
+    case kBF16:
+      hipLaunchKernelGGL(rope_table_kernel<__bf16>, grid, dim3(256), 0, st, (__bf16*)cos_out, (__bf16*)sin_out, f, T_, half);
+      break;
+    case kFP16:
+      hipLaunchKernelGGL(rope_table_kernel<_Float16>, grid, dim3(256), 0, st, (_Float16*)cos_out, (_Float16*)sin_out, f, T_, half);
+      break;
+    case kFP32:
+      hipLaunchKernelGGL(rope_table_kernel<float>, grid, dim3(256), 0, st, (float*)cos_out, (float*)sin_out, f, T_, half);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace sbda

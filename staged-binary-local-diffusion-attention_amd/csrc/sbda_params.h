@@ -1,0 +1,58 @@
+// Kernel parameter block and host-side launcher declarations.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sbda {
+
+// A [B, heads, T, D] view with element strides; the D stride is 1.
+struct View {
+  const void* p;
+  int64_t sb, sh, st;
+};
+
+struct MutView {
+  void* p;
+  int64_t sb, sh, st;
+};
+
+constexpr int kMaxSlots = 4;
+
+struct Params {
+  View q, k, v, dout;          // q and k are the raw (pre-prologue) rows when the prologue is fused
+  MutView o, dq, dk, dv;
+  float* lse;                  // [B, H, T] fp32, contiguous
+  int B, H, Hkv, group, T, D, S;
+  int off[kMaxSlots];
+  float scale;
+  // Fused prologue (head-RMSNorm + RoPE); unused otherwise.
+  const float* wq;             // [D] fp32
+  const float* wk;             // [D] fp32
+  const void* rope_cos;        // [T, D/2] activation dtype
+  const void* rope_sin;
+  float eps;
+  float* dwq_part;             // [parts, D] fp32 per-block partial sums
+  float* dwk_part;
+};
+
+enum DType : int { kBF16 = 0, kFP16 = 1, kFP32 = 2 };
+
+// Launchers return hipSuccess or the launch error.  `parts_*` report how
+// many per-block weight-gradient partial rows the backward writes.
+hipError_t launch_forward(const Params& p, int dtype, bool prologue, hipStream_t st);
+hipError_t launch_backward(const Params& p, int dtype, bool prologue, hipStream_t st);
+int64_t backward_partials(const Params& p, int dtype, bool prologue, int64_t* parts_q, int64_t* parts_k);
+hipError_t launch_reduce_partials(const float* part, int64_t parts, int D, float* out, hipStream_t st);
+hipError_t launch_rope_table(void* cos_out, void* sin_out, const float* inv_freq_host,
+                             int64_t T, int half, int dtype, hipStream_t st);
+
+// Lanes per row for head_dim D of element size esz (16 bytes per lane).
+inline int lanes_per_row(int D, int esz) {
+  int chunks = (D * esz + 15) / 16;
+  int l = 1;
+  while (l < chunks) l <<= 1;
+  return l;
+}
+
+}  // namespace sbda

@@ -1,0 +1,293 @@
+"""Fused SBDA attention ops: the drop-in boundary of the reference's fused path.
+
+``fused_sbda_key_backward(q, k, v, offsets) -> out`` keeps the signature of
+the reference (``BiAttn/sbda_triton.py:1468-1475``), called from
+``BiAttn/left_v2.py:268-294``: q, k, v are ``[B, H, T, D]`` tensors (usually
+permuted views of ``[B, T, H, D]`` memory), ``offsets`` the layer's int32
+offset buffer, and the result a new ``[B, H, T, D]`` tensor with q's dtype
+and strides.  The forward saves one fp32 log-normaliser per row; the
+backward writes each gradient row once (deterministic, no atomics).
+
+``fused_sbda``, ``fused_sbda_block`` and ``fused_sbda_block_full`` -- the
+reference's other backward variants of the same maths
+(``sbda_triton.py:1437-1466``) -- are the same op here, and
+``fused_sbda_gqa_key_backward`` accepts ``k``/``v`` with fewer heads
+(``sbda_triton.py:1477-1493``).
+
+``fused_sbda_prologue`` additionally fuses the per-head RMSNorm and RoPE of
+``BiAttn/left_v2.py:237-239`` into the kernels.
+
+Errors follow the reference's classes (``sbda_triton.py:1295-1302``):
+``RuntimeError`` for a non-GPU tensor, ``ValueError`` for shapes / source
+counts, ``TypeError`` for dtypes.  A missing library raises
+``SBDALibraryError`` (a ``RuntimeError``); nothing falls back to another
+implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import weakref
+from collections import OrderedDict
+from typing import Sequence
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
+# ------------------------------------------------------------------ helpers
+
+_OFFSET_CACHE: dict[int, tuple[weakref.ref, int, tuple[int, ...]]] = {}
+
+
+def host_offsets(offsets) -> tuple[int, ...]:
+    """Offsets as host ints.  A device tensor is read once (one sync) and
+    cached until it is modified or freed."""
+    if isinstance(offsets, torch.Tensor):
+        if offsets.ndim != 1:
+            raise ValueError("offsets must be a 1-D tensor")
+        key = id(offsets)
+        hit = _OFFSET_CACHE.get(key)
+        if hit is not None and hit[0]() is offsets and hit[1] == offsets._version:
+            return hit[2]
+        vals = tuple(int(x) for x in offsets.detach().to("cpu", torch.int64).tolist())
+        _OFFSET_CACHE[key] = (weakref.ref(offsets, lambda _r, k=key: _OFFSET_CACHE.pop(k, None)),
+                              offsets._version, vals)
+        return vals
+    return tuple(int(x) for x in offsets)
+
+
+def _kernel_view(t: torch.Tensor) -> torch.Tensor:
+    """``t`` if the kernels can read it in place, else a contiguous copy."""
+    esz = t.element_size()
+    ok = (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+          and all((s * esz) % 16 == 0 for s in t.stride()[:-1]))
+    return t if ok else t.contiguous()
+
+
+def _stream(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _validate(q, k, v, offs: Sequence[int], *, gqa: bool) -> None:
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise RuntimeError("fused SBDA requires ROCm device tensors")
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("q, k, and v must have [B,H,L,D] shapes")
+    if gqa:
+        if k.shape != v.shape or q.shape[0] != k.shape[0] or q.shape[2:] != k.shape[2:]:
+            raise ValueError("q/k/v sequence and head dimensions must match")
+        if k.shape[1] <= 0 or q.shape[1] % k.shape[1]:
+            raise ValueError("query heads must be divisible by kv heads")
+    elif q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("q, k, and v must have matching [B,H,L,D] shapes")
+    if len(offs) not in (2, 4):
+        raise ValueError("fused SBDA supports two or four sources")
+    if any(o < 0 for o in offs):
+        raise ValueError("SBDA offsets must be non-negative")
+    if q.dtype not in _DTYPES:
+        raise TypeError("unsupported SBDA dtype")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError("q, k and v must share one dtype")
+    if k.device != q.device or v.device != q.device:
+        raise ValueError("q, k and v must be on one device")
+
+
+def _shape_args(q, k, offs):
+    b, h, t, d = q.shape
+    return (b, h, k.shape[1], t, d, _DTYPES[q.dtype], _lib.offsets_array(offs), len(offs))
+
+
+# -------------------------------------------------------- raw entry points
+
+def sbda_forward(q, k, v, offsets) -> tuple[torch.Tensor, torch.Tensor]:
+    """Forward without autograd: ``(out [B,H,T,D], lse [B,H,T] fp32)``."""
+    offs = host_offsets(offsets)
+    _validate(q, k, v, offs, gqa=True)
+    lib = _lib.load()
+    q, k, v = (_kernel_view(x) for x in (q, k, v))
+    out = torch.empty_like(q)
+    b, h, t, _ = q.shape
+    lse = torch.empty((b, h, t), dtype=torch.float32, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.sbda_forward(
+            _ptr(q), _lib.strides(q), _ptr(k), _lib.strides(k), _ptr(v), _lib.strides(v),
+            _ptr(out), _lib.strides(out), _ptr(lse), *_shape_args(q, k, offs), _stream(q)))
+    return out, lse
+
+
+def sbda_backward(q, k, v, grad_out, lse, offsets):
+    """Backward without autograd: ``(dq, dk, dv)`` from saved ``lse``."""
+    offs = host_offsets(offsets)
+    _validate(q, k, v, offs, gqa=True)
+    lib = _lib.load()
+    q, k, v, grad_out = (_kernel_view(x) for x in (q, k, v, grad_out))
+    if grad_out.shape != q.shape or grad_out.dtype != q.dtype:
+        raise ValueError("grad_out must match q's shape and dtype")
+    lse = lse.contiguous()
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.sbda_backward(
+            _ptr(q), _lib.strides(q), _ptr(k), _lib.strides(k), _ptr(v), _lib.strides(v),
+            _ptr(grad_out), _lib.strides(grad_out), _ptr(lse),
+            _ptr(dq), _lib.strides(dq), _ptr(dk), _lib.strides(dk), _ptr(dv), _lib.strides(dv),
+            *_shape_args(q, k, offs), _stream(q)))
+    return dq, dk, dv
+
+
+# ----------------------------------------------------------------- autograd
+
+class _FusedSBDAKeyBackward(torch.autograd.Function):
+    """O + per-row LSE forward; gather-form, atomic-free backward."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, offsets):
+        out, lse = sbda_forward(q, k, v, offsets)
+        ctx.save_for_backward(_kernel_view(q), _kernel_view(k), _kernel_view(v), lse)
+        ctx.offs = host_offsets(offsets)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        q, k, v, lse = ctx.saved_tensors
+        dq, dk, dv = sbda_backward(q, k, v, grad_out, lse, ctx.offs)
+        return dq, dk, dv, None
+
+
+def fused_sbda_key_backward(q, k, v, offsets):
+    """Fused SBDA attention, ``[B,H,T,D]`` in and out (``sbda_triton.py:1468-1475``)."""
+    if k.shape != q.shape or v.shape != q.shape:
+        raise ValueError("q, k, and v must have matching [B,H,L,D] shapes")
+    return _FusedSBDAKeyBackward.apply(q, k, v, offsets)
+
+
+def fused_sbda_gqa_key_backward(q, k, v, offsets):
+    """Fused SBDA with ``k``/``v`` at ``kv_heads`` (``sbda_triton.py:1477-1493``)."""
+    return _FusedSBDAKeyBackward.apply(q, k, v, offsets)
+
+
+# The reference's token/block backward variants compute the same maths with
+# other (atomic) backward kernels; here they are the one deterministic op.
+fused_sbda = fused_sbda_key_backward
+fused_sbda_block = fused_sbda_key_backward
+fused_sbda_block_full = fused_sbda_key_backward
+
+
+# ------------------------------------------------------- fused prologue op
+
+_ROPE_CACHE: "OrderedDict[tuple, tuple[torch.Tensor, torch.Tensor]]" = OrderedDict()
+_ROPE_CACHE_LIMIT = 4
+
+
+def rope_inverse_frequencies(head_dim: int, theta: float) -> torch.Tensor:
+    """``theta ** (-arange(0, D, 2) / D)`` in fp32 on the CPU, the expression of
+    ``BiAttn/attention_common.py:16-17``, so angles match the reference bit for bit."""
+    idx = torch.arange(0, head_dim, 2, dtype=torch.float32)
+    return theta ** (-idx / head_dim)
+
+
+def rope_tables(length: int, head_dim: int, theta: float, dtype: torch.dtype,
+                device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+    """Device ``[length, head_dim/2]`` cos/sin tables in ``dtype`` (cached)."""
+    device = torch.device(device)
+    key = (device, int(length), int(head_dim), float(theta), dtype)
+    hit = _ROPE_CACHE.get(key)
+    if hit is not None:
+        _ROPE_CACHE.move_to_end(key)
+        return hit
+    inv = rope_inverse_frequencies(head_dim, theta).contiguous()
+    cos = torch.empty((length, head_dim // 2), dtype=dtype, device=device)
+    sin = torch.empty_like(cos)
+    lib = _lib.load()
+    with torch.cuda.device(device):
+        _lib.check(lib.sbda_rope_table(
+            _ptr(cos), _ptr(sin), ctypes.cast(inv.data_ptr(), ctypes.POINTER(ctypes.c_float)),
+            length, head_dim, _DTYPES[dtype], ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)))
+    _ROPE_CACHE[key] = (cos, sin)
+    while len(_ROPE_CACHE) > _ROPE_CACHE_LIMIT:
+        _ROPE_CACHE.popitem(last=False)
+    return cos, sin
+
+
+def _weight32(w: torch.Tensor, d: int, device) -> torch.Tensor:
+    if w.shape != (d,):
+        raise ValueError(f"norm weight must have shape ({d},)")
+    return w.detach().to(device=device, dtype=torch.float32).contiguous()
+
+
+class _FusedSBDAPrologue(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q_raw, k_raw, v, q_weight, k_weight, offsets, theta, eps):
+        offs = host_offsets(offsets)
+        _validate(q_raw, k_raw, v, offs, gqa=True)
+        lib = _lib.load()
+        q, k, v = (_kernel_view(x) for x in (q_raw, k_raw, v))
+        b, h, t, d = q.shape
+        wq, wk = _weight32(q_weight, d, q.device), _weight32(k_weight, d, q.device)
+        cos, sin = rope_tables(t, d, theta, q.dtype, q.device)
+        out = torch.empty_like(q)
+        lse = torch.empty((b, h, t), dtype=torch.float32, device=q.device)
+        with torch.cuda.device(q.device):
+            _lib.check(lib.sbda_forward_prologue(
+                _ptr(q), _lib.strides(q), _ptr(k), _lib.strides(k), _ptr(v), _lib.strides(v),
+                _ptr(out), _lib.strides(out), _ptr(lse), _ptr(wq), _ptr(wk), _ptr(cos), _ptr(sin),
+                float(eps), *_shape_args(q, k, offs), _stream(q)))
+        ctx.save_for_backward(q, k, v, wq, wk, lse, cos, sin)
+        ctx.offs, ctx.eps = offs, float(eps)
+        ctx.wdtypes = (q_weight.dtype, k_weight.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        q, k, v, wq, wk, lse, cos, sin = ctx.saved_tensors
+        offs = ctx.offs
+        lib = _lib.load()
+        g = _kernel_view(grad_out)
+        if g.dtype != q.dtype:
+            g = g.to(q.dtype)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        d = q.shape[-1]
+        dwq = torch.empty(d, dtype=torch.float32, device=q.device)
+        dwk = torch.empty_like(dwq)
+        shape = _shape_args(q, k, offs)
+        need = lib.sbda_backward_prologue_workspace(*shape)
+        if need < 0:
+            _lib.check(-need)
+        ws = torch.empty(max(int(need), 16), dtype=torch.uint8, device=q.device)
+        with torch.cuda.device(q.device):
+            _lib.check(lib.sbda_backward_prologue(
+                _ptr(q), _lib.strides(q), _ptr(k), _lib.strides(k), _ptr(v), _lib.strides(v),
+                _ptr(g), _lib.strides(g), _ptr(lse), _ptr(wq), _ptr(wk), _ptr(cos), _ptr(sin),
+                ctx.eps, _ptr(dq), _lib.strides(dq), _ptr(dk), _lib.strides(dk),
+                _ptr(dv), _lib.strides(dv), _ptr(dwq), _ptr(dwk), _ptr(ws), ws.numel(),
+                *shape, _stream(q)))
+        return (dq, dk, dv, dwq.to(ctx.wdtypes[0]), dwk.to(ctx.wdtypes[1]),
+                None, None, None)
+
+
+def fused_sbda_prologue(q_raw, k_raw, v, offsets, q_weight, k_weight, *,
+                        theta: float, eps: float = 1e-6):
+    """Head-RMSNorm(q, k) -> RoPE -> SBDA attention in one fused op.
+
+    ``q_raw``: ``[B, H, T, D]`` projections before normalisation; ``k_raw``,
+    ``v``: ``[B, Hkv, T, D]``; ``q_weight``/``k_weight``: ``[D]`` norm
+    weights.  Equals ``fused_sbda_key_backward(rope(norm(q)), rope(norm(k)),
+    v, offsets)`` with the reference's prologue (``BiAttn/left_v2.py:237-239``).
+    """
+    return _FusedSBDAPrologue.apply(q_raw, k_raw, v, q_weight, k_weight, offsets,
+                                    float(theta), float(eps))
+
+
+__all__ = [
+    "fused_sbda", "fused_sbda_block", "fused_sbda_block_full",
+    "fused_sbda_key_backward", "fused_sbda_gqa_key_backward",
+    "fused_sbda_prologue", "host_offsets", "rope_inverse_frequencies", "rope_tables",
+    "sbda_backward", "sbda_forward",
+]

@@ -1,0 +1,281 @@
+"""GPU parity of the HIP kernels against the CPU oracle (through the C ABI).
+
+Bars (from the build's north star): fp32 outputs within 1e-5 relative;
+bf16/fp16 outputs and gradients within 2e-2 relative and 1e-2 absolute of an
+fp32 oracle run on the same (rounded) inputs; source indexing and masks
+bit-exact (checked by exact-integer probes).  Inputs are generated on the CPU
+from fixed seeds, so both sides see identical bits.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+import sbda_amd
+from oracle import sbda_oracle as ref
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+FP32_TOL = dict(rtol=1e-5, atol=1e-5)
+LOW_TOL = dict(rtol=2e-2, atol=1e-2)
+
+
+def _inputs(b, t, h, d, dtype, seed, hkv=None, n=4):
+    """n tensors ``[B, T, heads, D]`` (CPU, ``dtype``), N(0, 1) from one seed."""
+    g = torch.Generator().manual_seed(seed)
+    heads = [h, hkv or h, hkv or h, h][:n]
+    return [torch.randn(b, t, hh, d, generator=g).to(dtype) for hh in heads]
+
+
+def _dev(x):
+    """CPU [B,T,H,D] -> device [B,H,T,D] view (the left_v2 layout)."""
+    return x.to(DEV).permute(0, 2, 1, 3)
+
+
+def _fused(q, k, v, offs, grad):
+    qd, kd, vd = (_dev(x).requires_grad_() for x in (q, k, v))
+    off = torch.tensor(offs, dtype=torch.int32, device=DEV)
+    out = sbda_amd.fused_sbda_gqa_key_backward(qd, kd, vd, off)
+    out.backward(_dev(grad))
+    torch.cuda.synchronize()
+    return [x.detach().float().cpu() for x in (out, qd.grad, kd.grad, vd.grad)]
+
+
+def _oracle(q, k, v, offs, grad, dtype=torch.float32):
+    rq, rk, rv = (x.to(dtype).permute(0, 2, 1, 3).requires_grad_() for x in (q, k, v))
+    out = ref.gather_attention(rq, rk, rv, offs)
+    out.backward(grad.to(dtype).permute(0, 2, 1, 3))
+    return [x.detach().float() for x in (out, rq.grad, rk.grad, rv.grad)]
+
+
+def _close(got, want, tol, what):
+    for name, a, b in zip(("out", "dq", "dk", "dv"), got, want):
+        torch.testing.assert_close(a, b, **tol, msg=lambda m: f"{what} {name}: {m}")
+
+
+# ------------------------------------------------------------ fp32 parity
+
+@pytest.mark.parametrize("layer", [1, 2, 3])
+def test_config1_fp32_matches_oracle(layer):
+    # B=1, T=32, H=2, head_dim=8, fp32, layers 1..3.
+    q, k, v, g = _inputs(1, 32, 2, 8, torch.float32, seed=100 + layer)
+    offs = ref.sbda_layer_offsets(layer)
+    got = _fused(q, k, v, offs, g)
+    want = _oracle(q, k, v, offs, g, torch.float64)
+    _close(got, [w.float() for w in want], FP32_TOL, f"config1 layer {layer}")
+    out, lse = sbda_amd.sbda_forward(_dev(q), _dev(k), _dev(v), offs)
+    want_lse = ref.attention_lse(q.double().permute(0, 2, 1, 3), k.double().permute(0, 2, 1, 3), offs)
+    torch.testing.assert_close(lse.cpu().double(), want_lse, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("offs", [(0, 1, 2, 64), (0, 1, 2, 4096), (0, 2), (0, 5, 1, 300)])
+def test_fp32_head_dim_64(offs):
+    q, k, v, g = _inputs(2, 300, 4, 64, torch.float32, seed=7)
+    _close(_fused(q, k, v, offs, g), _oracle(q, k, v, offs, g), FP32_TOL, f"fp32 {offs}")
+
+
+# ------------------------------------------------------------ bf16 / fp16
+
+@pytest.mark.parametrize("layer", range(1, 13))
+def test_config2_bf16_forward_sweep(layer):
+    # B=8, T=4096, H=8, D=64, bf16, layers 1..12.
+    q, k, v = _inputs(8, 4096, 8, 64, torch.bfloat16, seed=200 + layer, n=3)
+    offs = ref.sbda_layer_offsets(layer)
+    out, lse = sbda_amd.sbda_forward(_dev(q), _dev(k), _dev(v), offs)
+    rq, rk, rv = (x.float().permute(0, 2, 1, 3) for x in (q, k, v))
+    want = ref.gather_attention(rq, rk, rv, offs)
+    torch.testing.assert_close(out.float().cpu(), want, **LOW_TOL)
+    torch.testing.assert_close(lse.cpu(), ref.attention_lse(rq, rk, offs), rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("layer", [1, 2, 3, 5, 8, 11, 12])
+def test_bf16_fwd_bwd_layers(layer):
+    q, k, v, g = _inputs(2, 2048, 8, 64, torch.bfloat16, seed=300 + layer)
+    offs = ref.sbda_layer_offsets(layer)
+    _close(_fused(q, k, v, offs, g), _oracle(q, k, v, offs, g), LOW_TOL, f"bf16 layer {layer}")
+
+
+def test_fp16_fwd_bwd():
+    q, k, v, g = _inputs(1, 1000, 8, 64, torch.float16, seed=17)
+    offs = (0, 1, 2, 16)
+    _close(_fused(q, k, v, offs, g), _oracle(q, k, v, offs, g), LOW_TOL, "fp16")
+
+
+@pytest.mark.parametrize("length,offs", [(1, (0, 1)), (7, (0, 1, 2, 1024)), (129, (0, 1, 2, 4))])
+def test_reference_kernel_test_cases_gqa_head_dim_40(length, offs):
+    # tests/test_model.py:46-68: GQA 4 query / 2 kv heads, head_dim 40, bf16.
+    q, k, v, g = _inputs(1, length, 4, 40, torch.bfloat16, seed=42, hkv=2)
+    got = _fused(q, k, v, offs, g)
+    want = _oracle(q, k, v, offs, g)
+    _close(got, want, LOW_TOL, f"gqa T={length}")
+    _close(got, want, dict(rtol=0.015, atol=0.015), f"gqa T={length} (reference tol)")
+
+
+# ------------------------------------------------- indexing and mask probes
+
+@pytest.mark.parametrize("offs", [(0, 1), (0, 2), (0, 1, 2, 4), (0, 1, 2, 512), (0, 1, 2, 4096),
+                                  (3, 1, 0, 7)])
+def test_source_indexing_is_exact(offs):
+    # q = 0 gives uniform weights over the valid sources, so with integer
+    # position codes in v the output times the source count is an exact
+    # integer sum of source positions, and exp(lse) is the exact count.
+    t, d = 2048, 8
+    q = torch.zeros(1, t, 2, d)
+    k = _inputs(1, t, 2, d, torch.float32, seed=5, n=1)[0]
+    pos = torch.arange(t, dtype=torch.float32)
+    v = torch.zeros(1, t, 2, d)
+    v[0, :, :, 0] = pos[:, None]
+    v[0, :, :, 1] = (pos * pos)[:, None]
+    v[0, :, :, 2] = 1.0
+    out, lse = sbda_amd.sbda_forward(_dev(q), _dev(k), _dev(v), offs)
+    out, lse = out.cpu().double(), lse.cpu().double()
+    _, valid = ref.path_tables(t, offs)
+    idx = torch.arange(t)[:, None] - torch.tensor(offs)[None, :]
+    count = valid.sum(-1).double()
+    s1 = (idx * valid).sum(-1).double()
+    s2 = (idx * idx * valid).sum(-1).double()
+    got_count = torch.exp(lse[0, 0]).round()
+    assert torch.equal(got_count, count)
+    assert torch.equal((out[0, 0, :, 0] * count).round(), s1)
+    # Sums of squared positions reach ~1.7e7, past fp32's exact integers:
+    # compare them to within 2 (a wrong source moves them by >= 2 * i).
+    assert ((out[0, 0, :, 1] * count) - s2).abs().max().item() < 2.0
+    torch.testing.assert_close(out[0, 0, :, 2], torch.ones(t, dtype=torch.float64), rtol=0, atol=1e-6)
+
+
+def test_empty_rows_are_zero_with_infinite_lse():
+    q, k, v, g = _inputs(1, 16, 2, 64, torch.float32, seed=9)
+    offs = (1, 2)                                   # row 0 has no source
+    got = _fused(q, k, v, offs, g)
+    assert got[0][:, :, 0].abs().max().item() == 0
+    _, lse = sbda_amd.sbda_forward(_dev(q), _dev(k), _dev(v), offs)
+    assert torch.isinf(lse[:, :, 0]).all() and (lse[:, :, 0] > 0).all()
+    _close(got, _oracle(q, k, v, offs, g), FP32_TOL, "empty rows")
+
+
+# -------------------------------------------------- layout and determinism
+
+def test_strided_and_contiguous_layouts_agree():
+    q, k, v, g = _inputs(2, 512, 8, 64, torch.bfloat16, seed=11)
+    offs = (0, 1, 2, 32)
+    a = _fused(q, k, v, offs, g)
+    qc, kc, vc = (_dev(x).contiguous().requires_grad_() for x in (q, k, v))
+    out = sbda_amd.fused_sbda_key_backward(qc, kc, vc, torch.tensor(offs, dtype=torch.int32, device=DEV))
+    assert out.is_contiguous()
+    out.backward(_dev(g))                           # non-contiguous grad_out
+    b = [x.detach().float().cpu() for x in (out, qc.grad, kc.grad, vc.grad)]
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def test_output_keeps_query_strides():
+    q, k, v, _ = _inputs(1, 64, 8, 64, torch.bfloat16, seed=12)
+    out = sbda_amd.fused_sbda_key_backward(_dev(q), _dev(k), _dev(v),
+                                           torch.tensor((0, 1), dtype=torch.int32, device=DEV))
+    assert out.stride() == _dev(q).stride()
+
+
+def test_backward_is_bitwise_deterministic():
+    q, k, v, g = _inputs(1, 4096, 8, 64, torch.bfloat16, seed=13)
+    offs = (0, 1, 2, 256)
+    out, lse = sbda_amd.sbda_forward(_dev(q), _dev(k), _dev(v), offs)
+    first = sbda_amd.sbda_backward(_dev(q), _dev(k), _dev(v), _dev(g), lse, offs)
+    for _ in range(2):
+        again = sbda_amd.sbda_backward(_dev(q), _dev(k), _dev(v), _dev(g), lse, offs)
+        for x, y in zip(first, again):
+            assert torch.equal(x, y)
+
+
+# ------------------------------------------------------------ prologue
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, dict(rtol=1e-4, atol=1e-5)),
+                                       (torch.bfloat16, LOW_TOL)])
+@pytest.mark.parametrize("layer", [1, 2, 3, 7, 12])
+def test_prologue_matches_oracle(dtype, tol, layer):
+    # Config 3 style: q/k head-RMS-normalised, then RoPE base 10000.
+    theta = 10000.0
+    b, t, h, d = 2, 2048, 8, 64
+    q, k, v, g = _inputs(b, t, h, d, dtype, seed=400 + layer)
+    gen = torch.Generator().manual_seed(401)
+    wq = (1 + 0.1 * torch.randn(d, generator=gen))
+    wk = (1 + 0.1 * torch.randn(d, generator=gen))
+    offs = ref.sbda_layer_offsets(layer)
+    qd, kd, vd = (_dev(x).requires_grad_() for x in (q, k, v))
+    wqd, wkd = wq.to(DEV).requires_grad_(), wk.to(DEV).requires_grad_()
+    out = sbda_amd.fused_sbda_prologue(qd, kd, vd, torch.tensor(offs, dtype=torch.int32, device=DEV),
+                                       wqd, wkd, theta=theta)
+    out.backward(_dev(g))
+    torch.cuda.synchronize()
+    rq, rk, rv = (x.float().requires_grad_() for x in (q, k, v))
+    rwq, rwk = wq.clone().requires_grad_(), wk.clone().requires_grad_()
+    qq, kk = ref.prologue(rq, rk, rwq, rwk, theta)
+    want = ref.gather_attention(qq.permute(0, 2, 1, 3), kk.permute(0, 2, 1, 3), rv.permute(0, 2, 1, 3), offs)
+    want.backward(g.float().permute(0, 2, 1, 3))
+    pairs = [("out", out, want), ("dq", qd.grad, rq.grad.permute(0, 2, 1, 3)),
+             ("dk", kd.grad, rk.grad.permute(0, 2, 1, 3)), ("dv", vd.grad, rv.grad.permute(0, 2, 1, 3))]
+    for name, a, w in pairs:
+        torch.testing.assert_close(a.detach().float().cpu(), w.detach(), **tol,
+                                   msg=lambda m: f"prologue {name}: {m}")
+    # Weight gradients sum over B*T*H rows: compare relative to their scale.
+    for name, a, w in (("dwq", wqd.grad, rwq.grad), ("dwk", wkd.grad, rwk.grad)):
+        a = a.float().cpu()
+        scale = w.abs().max().item() + 1e-6
+        assert (a - w).abs().max().item() / scale < (2e-2 if dtype != torch.float32 else 1e-4), name
+
+
+# --------------------------------------------------- metric-size properties
+
+@pytest.mark.parametrize("layer", [3, 20])
+def test_metric_shape_sampled_rows(layer):
+    # T = 2**20, H = 8, D = 64 bf16: check 2048 sampled rows of the output and
+    # of each gradient against the oracle evaluated on those rows' sources.
+    t, h, d = 1 << 20, 8, 64
+    offs = ref.sbda_layer_offsets(layer)
+    gen = torch.Generator(device=DEV).manual_seed(500 + layer)
+    q, k, v, g = (torch.randn(1, t, h, d, generator=gen, device=DEV).to(torch.bfloat16) for _ in range(4))
+    qd, kd, vd = (x.permute(0, 2, 1, 3).requires_grad_() for x in (q, k, v))
+    out = sbda_amd.fused_sbda_key_backward(qd, kd, vd, torch.tensor(offs, dtype=torch.int32, device=DEV))
+    out.backward(g.permute(0, 2, 1, 3))
+    torch.cuda.synchronize()
+    rows = torch.cat([torch.arange(0, 8), torch.randint(0, t, (2040,), generator=torch.Generator().manual_seed(3))])
+    rows = rows.unique()
+    qf, kf, vf, gf = (x[0].float().cpu() for x in (q, k, v, g))   # [T, H, D]
+    scale = d ** -0.5
+
+    def weights(i):
+        src = [i - o for o in offs]
+        ok = torch.tensor([j >= 0 for j in src])
+        js = torch.tensor([max(j, 0) for j in src])
+        sc = (qf[i][None] * kf[js]).sum(-1) * scale          # [S, H]
+        sc = sc.masked_fill(~ok[:, None], -math.inf)
+        return js, ok, torch.softmax(sc, 0)
+
+    got_o = out.detach()[0].permute(1, 0, 2).float().cpu()
+    got_dq = qd.grad[0].permute(1, 0, 2).float().cpu()
+    got_dk = kd.grad[0].permute(1, 0, 2).float().cpu()
+    got_dv = vd.grad[0].permute(1, 0, 2).float().cpu()
+
+    def dS(i):
+        js, ok, p = weights(i)
+        dp = (gf[i][None] * vf[js]).sum(-1) * ok[:, None]
+        delta = (p * dp).sum(0, keepdim=True)
+        return js, ok, p, p * (dp - delta)
+
+    for i in rows.tolist():
+        js, ok, p, ds = dS(i)
+        o = (p[:, :, None] * vf[js]).sum(0)
+        dq = scale * (ds[:, :, None] * kf[js]).sum(0)
+        dk = torch.zeros(h, d)
+        dv = torch.zeros(h, d)
+        for s, o_s in enumerate(offs):
+            qi = i + o_s
+            if qi < t:
+                _, _, pq, dsq = dS(qi)
+                dk += scale * dsq[s][:, None] * qf[qi]
+                dv += pq[s][:, None] * gf[qi]
+        for name, a, w in (("out", got_o[i], o), ("dq", got_dq[i], dq), ("dk", got_dk[i], dk), ("dv", got_dv[i], dv)):
+            torch.testing.assert_close(a, w, **LOW_TOL, msg=lambda m: f"row {i} {name}: {m}")

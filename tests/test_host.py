@@ -1,0 +1,127 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports
+exactly what ``include/sbda_amd.h`` declares, argument validation maps to the
+reference's error classes, the schedule matches the reference's known answers
+and the module mirrors the reference's constructor/parameter surface."""
+
+from __future__ import annotations
+
+import ctypes
+import json
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import sbda_amd
+from sbda_amd import _lib
+from oracle import sbda_oracle as ref
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "sbda_amd.h"
+KATS = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())
+
+
+def _declared_functions() -> set[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(sbda_[a-z_0-9]+)\s*\(", text))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = _declared_functions()
+    assert declared == set(_lib.SIGNATURES), "binding and header disagree"
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.sbda_abi_version() == _lib.ABI_VERSION
+
+
+def _shape_call(lib, **kw):
+    args = dict(batch=1, heads=2, kv_heads=2, length=8, head_dim=64, dtype=0,
+                offsets=(0, 1, 2, 4))
+    args.update(kw)
+    offs = args["offsets"]
+    return lib.sbda_backward_prologue_workspace(
+        args["batch"], args["heads"], args["kv_heads"], args["length"], args["head_dim"],
+        args["dtype"], _lib.offsets_array(offs), len(offs))
+
+
+def test_validation_errors_without_launching():
+    lib = _lib.load()
+    assert _shape_call(lib) > 0
+    assert _shape_call(lib, dtype=7) == -_lib.ERR_DTYPE
+    assert "dtype" in lib.sbda_last_error().decode()
+    assert _shape_call(lib, head_dim=12) == -_lib.ERR_VALUE       # 24 bytes per row
+    assert _shape_call(lib, heads=3, kv_heads=2) == -_lib.ERR_VALUE
+    assert _shape_call(lib, offsets=(0, -1)) == -_lib.ERR_VALUE
+    assert _shape_call(lib, offsets=(0, 1, 2, 3, 4)) == -_lib.ERR_VALUE
+    assert _shape_call(lib, length=0) == -_lib.ERR_VALUE
+    # A null tensor is rejected before anything is launched.
+    z = ctypes.c_void_p(0)
+    st = (ctypes.c_int64 * 4)(0, 0, 0, 1)
+    rc = lib.sbda_forward(z, st, z, st, z, st, z, st, z, 1, 1, 1, 8, 64, 0,
+                          _lib.offsets_array((0, 1)), 2, z)
+    assert rc == _lib.ERR_VALUE and "null" in lib.sbda_last_error().decode()
+    with pytest.raises(ValueError):
+        _lib.check(_lib.ERR_VALUE)
+    with pytest.raises(TypeError):
+        _lib.check(_lib.ERR_DTYPE)
+
+
+def test_python_op_rejects_cpu_tensors_like_the_reference():
+    q = torch.zeros(1, 2, 8, 64)
+    with pytest.raises(RuntimeError):
+        sbda_amd.fused_sbda_key_backward(q, q, q, torch.tensor([0, 1], dtype=torch.int32))
+
+
+def test_host_offsets_cache():
+    t = torch.tensor([0, 1, 2, 8], dtype=torch.int32)
+    assert sbda_amd.host_offsets(t) == (0, 1, 2, 8)
+    t[3] = 16                                   # bumps the version counter
+    assert sbda_amd.host_offsets(t) == (0, 1, 2, 16)
+    assert sbda_amd.host_offsets([0, 2]) == (0, 2)
+
+
+def test_topology_matches_oracle_and_reference_statistics():
+    for layer in range(1, 24):
+        assert sbda_amd.topology_offsets(layer, topology="sbda") == ref.sbda_layer_offsets(layer)
+        assert sbda_amd.sbda_stage(layer) == ref.sbda_stage(layer)
+    stats = KATS["route_graph_statistics"]
+    for name, length, layers, cov, auc, total, unique in stats["rows"]:
+        offs = [sbda_amd.topology_offsets(l, topology=name, total_layers=layers)
+                for l in range(1, layers + 1)]
+        assert ref.valid_cell_count(length, offs) == total, name
+        assert ref.unique_cell_count(length, offs) == unique, name
+        reach, area = {0}, 0
+        for o in offs:
+            reach = {r + x for r in reach for x in o if r + x < length}
+            area += len(reach)
+        assert (len(reach), area) == (cov, auc), name
+    with pytest.raises(ValueError):
+        sbda_amd.topology_offsets(0, topology="sbda")
+    with pytest.raises(ValueError):
+        sbda_amd.topology_offsets(1, topology="nope")
+
+
+def test_module_surface_matches_reference():
+    m = sbda_amd.SBDAttention(64, 4, 3, kv_heads=2)
+    assert sorted(m.state_dict()) == sorted(
+        ["q.weight", "k.weight", "v.weight", "q_norm.weight", "k_norm.weight", "out.weight"])
+    assert m.topology == "sbda" and m.backward_mode == "key"
+    assert m._fused_offsets.tolist() == [0, 1, 2, 4]
+    assert m._fused_offsets.dtype == torch.int32
+    with pytest.raises(ValueError):
+        sbda_amd.SBDAttention(30, 4, 1)
+    with pytest.raises(ValueError):
+        sbda_amd.SBDAttention(32, 4, 0)
+    with pytest.raises(ValueError):
+        sbda_amd.BinaryPathAttention(32, 4, 1, backward_mode="other")
+    with pytest.raises(ValueError):
+        sbda_amd.SBDAttention(32, 4, 1, kv_heads=3)
+    x = torch.randn(1, 5, 64)
+    with pytest.raises(NotImplementedError, match="CPU tensor"):
+        m(x)
+    with pytest.raises(ValueError):
+        m(torch.randn(1, 5, 32))
+    assert sbda_amd.SBDAAttention is sbda_amd.SBDAttention

@@ -93,8 +93,8 @@ int sbda_backward(const void* q, const int64_t* q_strides,
 /*
  * Forward with the head-RMSNorm + RoPE prologue fused: q_raw and k_raw are
  * the projections before normalisation; q_weight/k_weight are fp32 [D]
- * norm weights; rope_cos/rope_sin are [T, D/2] tables in the activation
- * dtype (sbda_rope_table).  eps is the norm epsilon (reference: 1e-6).
+ * norm weights; rope_cos/rope_sin are fp32 [T, D/2] tables
+ * (sbda_rope_table).  eps is the norm epsilon (reference: 1e-6).
  */
 int sbda_forward_prologue(const void* q_raw, const int64_t* q_strides,
                           const void* k_raw, const int64_t* k_strides,
@@ -102,7 +102,7 @@ int sbda_forward_prologue(const void* q_raw, const int64_t* q_strides,
                           void* out, const int64_t* out_strides,
                           float* lse,
                           const float* q_weight, const float* k_weight,
-                          const void* rope_cos, const void* rope_sin, float eps,
+                          const float* rope_cos, const float* rope_sin, float eps,
                           int64_t batch, int64_t heads, int64_t kv_heads,
                           int64_t length, int64_t head_dim, int32_t dtype,
                           const int32_t* offsets, int32_t num_offsets,
@@ -124,7 +124,7 @@ int sbda_backward_prologue(const void* q_raw, const int64_t* q_strides,
                            const void* dout, const int64_t* dout_strides,
                            const float* lse,
                            const float* q_weight, const float* k_weight,
-                           const void* rope_cos, const void* rope_sin, float eps,
+                           const float* rope_cos, const float* rope_sin, float eps,
                            void* dq_raw, const int64_t* dq_strides,
                            void* dk_raw, const int64_t* dk_strides,
                            void* dv, const int64_t* dv_strides,
@@ -137,11 +137,11 @@ int sbda_backward_prologue(const void* q_raw, const int64_t* q_strides,
 
 /*
  * RoPE tables: cos/sin[t, i] = cos/sin(fl32(t * inv_freq[i])) for t < length,
- * i < head_dim/2, stored in `dtype`.  inv_freq is a host fp32 array of
- * head_dim/2 values (head_dim <= 512).
+ * i < head_dim/2, as fp32 [length, head_dim/2].  inv_freq is a host fp32
+ * array of head_dim/2 values (head_dim <= 512).
  */
-int sbda_rope_table(void* rope_cos, void* rope_sin, const float* inv_freq,
-                    int64_t length, int64_t head_dim, int32_t dtype, void* stream);
+int sbda_rope_table(float* rope_cos, float* rope_sin, const float* inv_freq,
+                    int64_t length, int64_t head_dim, void* stream);
 
 #ifdef __cplusplus
 }

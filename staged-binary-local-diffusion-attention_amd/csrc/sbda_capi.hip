@@ -110,7 +110,7 @@ int hip_status(hipError_t e, const char* what) {
 
 int forward_impl(bool pro, const void* q, const int64_t* qs, const void* k, const int64_t* ks,
                  const void* v, const int64_t* vs, void* out, const int64_t* os, float* lse,
-                 const float* wq, const float* wk, const void* rc, const void* rs, float eps,
+                 const float* wq, const float* wk, const float* rc, const float* rs, float eps,
                  int64_t batch, int64_t heads, int64_t kv_heads, int64_t length, int64_t head_dim,
                  int32_t dtype, const int32_t* offsets, int32_t n, void* stream) {
   g_error.clear();
@@ -147,8 +147,8 @@ void partials(const Params& p, int dtype, int64_t* pq, int64_t* pk) {
 
 int backward_impl(bool pro, const void* q, const int64_t* qs, const void* k, const int64_t* ks,
                   const void* v, const int64_t* vs, const void* dout, const int64_t* dos,
-                  const float* lse, const float* wq, const float* wk, const void* rc,
-                  const void* rs, float eps, void* dq, const int64_t* dqs, void* dk,
+                  const float* lse, const float* wq, const float* wk, const float* rc,
+                  const float* rs, float eps, void* dq, const int64_t* dqs, void* dk,
                   const int64_t* dks, void* dv, const int64_t* dvs, float* dwq, float* dwk,
                   void* ws, int64_t ws_bytes, int64_t batch, int64_t heads, int64_t kv_heads,
                   int64_t length, int64_t head_dim, int32_t dtype, const int32_t* offsets,
@@ -202,7 +202,7 @@ using namespace sbda;
 
 extern "C" {
 
-int sbda_abi_version(void) { return 1; }
+int sbda_abi_version(void) { return 2; }
 
 const char* sbda_last_error(void) { return g_error.c_str(); }
 
@@ -226,8 +226,8 @@ int sbda_backward(const void* q, const int64_t* qs, const void* k, const int64_t
 
 int sbda_forward_prologue(const void* q, const int64_t* qs, const void* k, const int64_t* ks,
                           const void* v, const int64_t* vs, void* out, const int64_t* os,
-                          float* lse, const float* wq, const float* wk, const void* rc,
-                          const void* rs, float eps, int64_t batch, int64_t heads,
+                          float* lse, const float* wq, const float* wk, const float* rc,
+                          const float* rs, float eps, int64_t batch, int64_t heads,
                           int64_t kv_heads, int64_t length, int64_t head_dim, int32_t dtype,
                           const int32_t* offsets, int32_t n, void* stream) {
   return forward_impl(true, q, qs, k, ks, v, vs, out, os, lse, wq, wk, rc, rs, eps, batch, heads,
@@ -248,8 +248,8 @@ int64_t sbda_backward_prologue_workspace(int64_t batch, int64_t heads, int64_t k
 
 int sbda_backward_prologue(const void* q, const int64_t* qs, const void* k, const int64_t* ks,
                            const void* v, const int64_t* vs, const void* dout, const int64_t* dos,
-                           const float* lse, const float* wq, const float* wk, const void* rc,
-                           const void* rs, float eps, void* dq, const int64_t* dqs, void* dk,
+                           const float* lse, const float* wq, const float* wk, const float* rc,
+                           const float* rs, float eps, void* dq, const int64_t* dqs, void* dk,
                            const int64_t* dks, void* dv, const int64_t* dvs, float* dwq,
                            float* dwk, void* ws, int64_t ws_bytes, int64_t batch, int64_t heads,
                            int64_t kv_heads, int64_t length, int64_t head_dim, int32_t dtype,
@@ -259,16 +259,14 @@ int sbda_backward_prologue(const void* q, const int64_t* qs, const void* k, cons
                        dtype, offsets, n, stream);
 }
 
-int sbda_rope_table(void* rope_cos, void* rope_sin, const float* inv_freq, int64_t length,
-                    int64_t head_dim, int32_t dtype, void* stream) {
+int sbda_rope_table(float* rope_cos, float* rope_sin, const float* inv_freq, int64_t length,
+                    int64_t head_dim, void* stream) {
   g_error.clear();
-  if (dtype != kBF16 && dtype != kFP16 && dtype != kFP32)
-    return fail(SBDA_ERR_DTYPE, "unsupported RoPE table dtype code %d", (int)dtype);
   if (!rope_cos || !rope_sin || !inv_freq) return fail(SBDA_ERR_VALUE, "RoPE table: null pointer");
-  if (length <= 0 || head_dim <= 0 || head_dim % 2 || head_dim > 512)
+  if (length <= 0 || length >= (int64_t(1) << 31) || head_dim <= 0 || head_dim % 2 || head_dim > 512)
     return fail(SBDA_ERR_VALUE, "RoPE table: bad length %lld or head_dim %lld", (long long)length,
                 (long long)head_dim);
-  hipError_t e = launch_rope_table(rope_cos, rope_sin, inv_freq, length, (int)(head_dim / 2), dtype,
+  hipError_t e = launch_rope_table(rope_cos, rope_sin, inv_freq, length, (int)(head_dim / 2),
                                    reinterpret_cast<hipStream_t>(stream));
   return hip_status(e, "sbda rope table launch");
 }

@@ -170,26 +170,35 @@ __device__ inline float fast_log(float x) { return __builtin_amdgcn_logf(x) * kL
 // BiAttn/attention_common.py:25-50 and :64-76):
 //   n = x * rsqrt(mean(x^2) + eps);  y = n * w;
 //   z[d] = y[d] cos[d] - y[d + D/2] sin[d],  z[d + D/2] = y[d + D/2] cos[d] + y[d] sin[d]
-// for d < D/2, with cos/sin read from a [T, D/2] table in the activation
-// dtype (the reference casts its tables to that dtype).  Products are
-// rounded one at a time (no contraction) to follow the reference's op order.
+// for d < D/2, with cos/sin read from fp32 [T, D/2] tables (the reference
+// evaluates them in fp32; its bf16 runs then round them, which the fp32
+// tables here do not).  Products are rounded one at a time (no
+// contraction) to follow the reference's op order.
 template <typename T, int LPR>
 struct Prologue {
   static constexpr int VEC = VecOf<T>::value;
   static constexpr int HV = VEC / 2;
 
-  // Loads this lane's HV cos and sin entries of position t.
-  __device__ static inline void load_cs(const T* __restrict__ cs_cos, const T* __restrict__ cs_sin,
-                                        int64_t t, int li, int D, float (&c)[HV], float (&s)[HV]) {
+  // Loads this lane's HV cos and sin entries of position t from fp32 tables.
+  __device__ static inline void load_cs(const float* __restrict__ cs_cos,
+                                        const float* __restrict__ cs_sin, int64_t t, int li, int D,
+                                        float (&c)[HV], float (&s)[HV]) {
     const int half = D >> 1;
     if (li * HV < half) {
-      // HV elements are 8 bytes for every dtype (4 x 16-bit or 2 x fp32).
-      const uint2 a = *reinterpret_cast<const uint2*>(cs_cos + t * half + li * HV);
-      const uint2 b = *reinterpret_cast<const uint2*>(cs_sin + t * half + li * HV);
-      const uint32_t wc[2] = {a.x, a.y};
-      const uint32_t ws[2] = {b.x, b.y};
-      unpack_words<T, 2>(wc, c);
-      unpack_words<T, 2>(ws, s);
+      const float* pc = cs_cos + t * half + li * HV;
+      const float* ps = cs_sin + t * half + li * HV;
+      if constexpr (HV == 4) {
+        const float4 a = *reinterpret_cast<const float4*>(pc);
+        const float4 b = *reinterpret_cast<const float4*>(ps);
+        c[0] = a.x; c[1] = a.y; c[2] = a.z; c[3] = a.w;
+        s[0] = b.x; s[1] = b.y; s[2] = b.z; s[3] = b.w;
+      } else {
+        static_assert(HV == 2, "16-bit rows hold 4, fp32 rows 2 elements per half");
+        const float2 a = *reinterpret_cast<const float2*>(pc);
+        const float2 b = *reinterpret_cast<const float2*>(ps);
+        c[0] = a.x; c[1] = a.y;
+        s[0] = b.x; s[1] = b.y;
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < HV; ++i) { c[i] = 1.f; s[i] = 0.f; }

@@ -43,7 +43,7 @@ __device__ inline void load_key(const Params& p, int b, int hk, int64_t t, int l
   if constexpr (PRO) {
     using PL = Prologue<T, LPR>;
     float c[PL::HV], s[PL::HV];
-    PL::load_cs((const T*)p.rope_cos, (const T*)p.rope_sin, t, li, p.D, c, s);
+    PL::load_cs(p.rope_cos, p.rope_sin, t, li, p.D, c, s);
     PL::forward(k, p.wk, c, s, li, p.D, p.eps);
   }
 }
@@ -103,7 +103,7 @@ __global__ __launch_bounds__(kBlock) void fwd_direct(Params p) {
   if constexpr (PRO) {
     using PL = Prologue<T, LPR>;
     float c[PL::HV], s[PL::HV];
-    PL::load_cs((const T*)p.rope_cos, (const T*)p.rope_sin, t, li, p.D, c, s);
+    PL::load_cs(p.rope_cos, p.rope_sin, t, li, p.D, c, s);
     PL::forward(q, p.wq, c, s, li, p.D, p.eps);
   }
 
@@ -162,7 +162,7 @@ __device__ inline void query_side(const Params& p, int b, int i, int h, int hk, 
   if constexpr (PRO) {
     using PL = Prologue<T, LPR>;
     float c[PL::HV], s[PL::HV];
-    PL::load_cs((const T*)p.rope_cos, (const T*)p.rope_sin, i, li, p.D, c, s);
+    PL::load_cs(p.rope_cos, p.rope_sin, i, li, p.D, c, s);
     PL::forward(q, p.wq, c, s, li, p.D, p.eps);
   }
   load_row<T, PRO>(row_ptr<T>(p.dout, b, h, i), li, p.D, go);
@@ -223,7 +223,7 @@ __global__ __launch_bounds__(kBlock) void bwd_dq_direct(Params p) {
     using PL = Prologue<T, LPR>;
     float x[VEC], c[PL::HV], s[PL::HV], dw[VEC];
     load_row<T, true>(row_ptr<T>(p.q, b, h, t), li, p.D, x);
-    PL::load_cs((const T*)p.rope_cos, (const T*)p.rope_sin, t, li, p.D, c, s);
+    PL::load_cs(p.rope_cos, p.rope_sin, t, li, p.D, c, s);
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) ss = __builtin_fmaf(x[e], x[e], ss);
@@ -285,7 +285,7 @@ __global__ __launch_bounds__(kBlock) void bwd_dkv_direct(Params p) {
     using PL = Prologue<T, LPR>;
     float x[VEC], c[PL::HV], s[PL::HV], dw[VEC];
     load_row<T, true>(row_ptr<T>(p.k, b, hk, j), li, p.D, x);
-    PL::load_cs((const T*)p.rope_cos, (const T*)p.rope_sin, j, li, p.D, c, s);
+    PL::load_cs(p.rope_cos, p.rope_sin, j, li, p.D, c, s);
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) ss = __builtin_fmaf(x[e], x[e], ss);
@@ -409,48 +409,36 @@ hipError_t launch_reduce_partials(const float* part, int64_t parts, int D, float
 
 // --------------------------------------------------------------- RoPE table
 //
-// cos/sin[t, i] = cos/sin(fl32(t * inv_freq[i])) cast to the activation
-// dtype: the reference builds angles as an fp32 outer product
-// (BiAttn/attention_common.py:18-21).  inv_freq is computed on the host with
-// the reference's own fp32 expression so the angles agree bit for bit.
+// cos/sin[t, i] = cos/sin(fl32(t * inv_freq[i])) in fp32: the reference
+// builds its angles as an fp32 outer product (BiAttn/attention_common.py:
+// 18-21); inv_freq is computed on the host with the reference's own fp32
+// expression so the angles agree bit for bit.
 struct InvFreq {
   float v[256];
 };
 
-template <typename T>
-__global__ __launch_bounds__(256) void rope_table_kernel(T* __restrict__ cos_out, T* __restrict__ sin_out,
-                                                         InvFreq f, int64_t T_, int half) {
+__global__ __launch_bounds__(256) void rope_table_kernel(float* __restrict__ cos_out,
+                                                         float* __restrict__ sin_out, InvFreq f,
+                                                         int64_t length, int half) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= T_ * half) return;
+  if (idx >= length * half) return;
   const int64_t t = idx / half;
   const int i = (int)(idx % half);
   const float ang = __fmul_rn((float)t, f.v[i]);
   float s, c;
   sincosf(ang, &s, &c);
-  cos_out[idx] = (T)c;
-  sin_out[idx] = (T)s;
+  cos_out[idx] = c;
+  sin_out[idx] = s;
 }
 
-hipError_t launch_rope_table(void* cos_out, void* sin_out, const float* inv_freq_host,
-                             int64_t T_, int half, int dtype, hipStream_t st) {
+hipError_t launch_rope_table(float* cos_out, float* sin_out, const float* inv_freq_host,
+                             int64_t length, int half, hipStream_t st) {
   if (half > 256) return hipErrorInvalidValue;
   InvFreq f;
   for (int i = 0; i < 256; ++i) f.v[i] = i < half ? inv_freq_host[i] : 0.f;
-  const int64_t n = T_ * half;
-  const dim3 grid((unsigned)((n + 255) / 256));
-  switch (dtype) {
-    case kBF16:
-      hipLaunchKernelGGL(rope_table_kernel<__bf16>, grid, dim3(256), 0, st, (__bf16*)cos_out, (__bf16*)sin_out, f, T_, half);
-      break;
-    case kFP16:
-      hipLaunchKernelGGL(rope_table_kernel<_Float16>, grid, dim3(256), 0, st, (_Float16*)cos_out, (_Float16*)sin_out, f, T_, half);
-      break;
-    case kFP32:
-      hipLaunchKernelGGL(rope_table_kernel<float>, grid, dim3(256), 0, st, (float*)cos_out, (float*)sin_out, f, T_, half);
-      break;
-    default:
-      return hipErrorInvalidValue;
-  }
+  const int64_t n = length * half;
+  hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                     cos_out, sin_out, f, length, half);
   return hipGetLastError();
 }
 

@@ -29,8 +29,8 @@ struct Params {
   // Fused prologue (head-RMSNorm + RoPE); unused otherwise.
   const float* wq;             // [D] fp32
   const float* wk;             // [D] fp32
-  const void* rope_cos;        // [T, D/2] activation dtype
-  const void* rope_sin;
+  const float* rope_cos;       // [T, D/2] fp32
+  const float* rope_sin;
   float eps;
   float* dwq_part;             // [parts, D] fp32 per-block partial sums
   float* dwk_part;
@@ -44,8 +44,8 @@ hipError_t launch_forward(const Params& p, int dtype, bool prologue, hipStream_t
 hipError_t launch_backward(const Params& p, int dtype, bool prologue, hipStream_t st);
 int64_t backward_partials(const Params& p, int dtype, bool prologue, int64_t* parts_q, int64_t* parts_k);
 hipError_t launch_reduce_partials(const float* part, int64_t parts, int D, float* out, hipStream_t st);
-hipError_t launch_rope_table(void* cos_out, void* sin_out, const float* inv_freq_host,
-                             int64_t T, int half, int dtype, hipStream_t st);
+hipError_t launch_rope_table(float* cos_out, float* sin_out, const float* inv_freq_host,
+                             int64_t length, int half, hipStream_t st);
 
 // Lanes per row for head_dim D of element size esz (16 bytes per lane).
 inline int lanes_per_row(int D, int esz) {

@@ -193,23 +193,26 @@ def rope_inverse_frequencies(head_dim: int, theta: float) -> torch.Tensor:
     return theta ** (-idx / head_dim)
 
 
-def rope_tables(length: int, head_dim: int, theta: float, dtype: torch.dtype,
+def rope_tables(length: int, head_dim: int, theta: float,
                 device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
-    """Device ``[length, head_dim/2]`` cos/sin tables in ``dtype`` (cached)."""
+    """Device fp32 ``[length, head_dim/2]`` cos/sin tables (cached).
+
+    Kept in fp32 for every activation dtype: the reference evaluates the
+    angles and their cos/sin in fp32 (``attention_common.py:18-21``)."""
     device = torch.device(device)
-    key = (device, int(length), int(head_dim), float(theta), dtype)
+    key = (device, int(length), int(head_dim), float(theta))
     hit = _ROPE_CACHE.get(key)
     if hit is not None:
         _ROPE_CACHE.move_to_end(key)
         return hit
     inv = rope_inverse_frequencies(head_dim, theta).contiguous()
-    cos = torch.empty((length, head_dim // 2), dtype=dtype, device=device)
+    cos = torch.empty((length, head_dim // 2), dtype=torch.float32, device=device)
     sin = torch.empty_like(cos)
     lib = _lib.load()
     with torch.cuda.device(device):
         _lib.check(lib.sbda_rope_table(
             _ptr(cos), _ptr(sin), ctypes.cast(inv.data_ptr(), ctypes.POINTER(ctypes.c_float)),
-            length, head_dim, _DTYPES[dtype], ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)))
+            length, head_dim, ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)))
     _ROPE_CACHE[key] = (cos, sin)
     while len(_ROPE_CACHE) > _ROPE_CACHE_LIMIT:
         _ROPE_CACHE.popitem(last=False)
@@ -231,7 +234,7 @@ class _FusedSBDAPrologue(torch.autograd.Function):
         q, k, v = (_kernel_view(x) for x in (q_raw, k_raw, v))
         b, h, t, d = q.shape
         wq, wk = _weight32(q_weight, d, q.device), _weight32(k_weight, d, q.device)
-        cos, sin = rope_tables(t, d, theta, q.dtype, q.device)
+        cos, sin = rope_tables(t, d, theta, q.device)
         out = torch.empty_like(q)
         lse = torch.empty((b, h, t), dtype=torch.float32, device=q.device)
         with torch.cuda.device(q.device):

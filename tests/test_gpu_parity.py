@@ -279,3 +279,15 @@ def test_metric_shape_sampled_rows(layer):
                 dv += pq[s][:, None] * gf[qi]
         for name, a, w in (("out", got_o[i], o), ("dq", got_dq[i], dq), ("dk", got_dk[i], dk), ("dv", got_dv[i], dv)):
             torch.testing.assert_close(a, w, **LOW_TOL, msg=lambda m: f"row {i} {name}: {m}")
+
+
+def test_rope_table_matches_fp32_reference_angles():
+    # Angles are fp32 products position * inv_freq (bit-identical to the
+    # reference's torch.outer); cos/sin then agree to a few fp32 ulps, also
+    # at the metric length where the angle reaches ~1e6 rad.
+    t, d = 1 << 20, 64
+    for theta in (10000.0, 1_000_000.0):
+        cos, sin = sbda_amd.rope_tables(t, d, theta, DEV)
+        want_c, want_s = ref.rope_tables(t, d, theta, torch.float32)
+        torch.testing.assert_close(cos.cpu(), want_c[:, : d // 2], rtol=0, atol=3e-7)
+        torch.testing.assert_close(sin.cpu(), want_s[:, : d // 2], rtol=0, atol=3e-7)

@@ -1,11 +1,683 @@
-// Wavefront-walk SBDA kernels (placeholder: not yet selected).
+// Wavefront-walk SBDA kernels: the fast path for the SBDA schedule.
+//
+// Layout.  One 64-lane wavefront holds all G = 64/LPR heads of one position
+// ("head group"): lane = g * LPR + li, so one 16-byte-per-lane load moves one
+// position's rows of the group (1 KiB for 8 heads x 64 dims x bf16).  Each
+// wave owns a tile of P consecutive positions and walks it in order.
+//
+// Sources.  Offsets split into "near" ones (0, 1, 2: a compile-time mask NM)
+// and at most one "far" offset F >= 3.  Near sources are the rows the walk
+// just loaded, kept in a 3-deep register rotation (no reload); the far
+// source is loaded directly.  Tiles are ordered so that the wave holding
+// positions t - F (and t + F) runs next to this one -- linear order for
+// F < P, column order (tile a, a + F, a + 2F, ...) otherwise -- and the
+// workgroup id is remapped so consecutive tiles share an XCD (and its L2).
+//
+// Backward (gather form, every row written once, no atomics).  Walking
+// queries u = a-2 .. end+1, the wave computes each query's weights p_s and
+// score gradients dS_s once; dQ_u is complete at once, and near-slot
+// contributions dK/dV_{u-n} += (scale dS_n q_u, p_n dO_u) go to three
+// rotating key accumulators.  Key j = u-2 is then complete except for its
+// far query i = j + F, whose weights are recomputed from q_i, dO_i, lse_i and
+// i's own sources (a second rotation over positions i, i-1, i-2, plus k_j,
+// v_j from the first).  Keys are written as soon as they complete.
+//
+// Reference semantics: BiAttn/left_v2.py:313-405 (forward maths) and the
+// key-centric backward specified by BiAttn/sbda_triton.py:507-671.
+
+#include <type_traits>
+
+#include "sbda_device.h"
 #include "sbda_params.h"
 
 namespace sbda {
 
-bool walk_applies(const Params&, int) { return false; }
-hipError_t walk_forward(const Params&, int, bool, hipStream_t) { return hipErrorInvalidValue; }
-hipError_t walk_backward(const Params&, int, bool, hipStream_t) { return hipErrorInvalidValue; }
-void walk_partials(const Params&, int, int64_t* pq, int64_t* pk) { *pq = 0; *pk = 0; }
+namespace {
+
+constexpr int kWaves = 4;               // independent waves per workgroup
+constexpr int kWalkBlock = kWaves * 64;
+
+struct WalkCfg {
+  int P;         // positions per tile
+  int HG;        // head groups (waves per position)
+  int tiles_t;   // tiles per (batch, head group) along T
+  int column;    // 1: column order (far offset F is a multiple of P)
+  int rows;      // column order: ceil(T / F)
+  int F;         // far offset (0 if none)
+  int nwg;       // workgroups in the grid
+  int64_t total; // tiles in the grid
+};
+
+// Workgroups are dealt to the 8 XCDs round-robin; give each XCD a contiguous
+// range of tiles instead.
+__device__ inline int64_t xcd_remap(int wg, int nwg) {
+  const int xcd = wg & 7, idx = wg >> 3, per = nwg >> 3, rem = nwg & 7;
+  return (int64_t)xcd * per + min(xcd, rem) + idx;
+}
+
+__device__ inline int64_t wave_id() {
+  return xcd_remap(blockIdx.x, gridDim.x) * kWaves + (threadIdx.x >> 6);
+}
+
+__device__ inline bool decode_tile(const Params& p, const WalkCfg& c, int64_t n, int& b, int& hg,
+                                   int& a) {
+  if (n >= c.total) return false;
+  hg = (int)(n % c.HG);
+  const int64_t rest = n / c.HG;
+  const int k = (int)(rest % c.tiles_t);
+  b = (int)(rest / c.tiles_t);
+  if (c.column) {
+    const int r = k % c.rows, cb = k / c.rows;
+    a = r * c.F + cb * c.P;
+  } else {
+    a = k * c.P;
+  }
+  return a < p.T;
+}
+
+template <typename T>
+struct Rows {
+  const T* __restrict__ base;
+  int64_t st;
+  __device__ inline const T* at(int64_t t) const { return base + t * st; }
+};
+
+template <typename T, int LPR, bool PRO>
+struct Lane {
+  static constexpr int VEC = VecOf<T>::value;
+  using PL = Prologue<T, LPR>;
+  int li;
+  int D;
+  const float* wq;
+  const float* wk;
+  const float* rc;
+  const float* rs;
+  float eps;
+
+  __device__ inline void init(const Params& p, int lane_in_row) {
+    li = lane_in_row;
+    D = p.D;
+    wq = p.wq;
+    wk = p.wk;
+    rc = p.rope_cos;
+    rs = p.rope_sin;
+    eps = p.eps;
+  }
+
+  __device__ inline void load(const Rows<T>& r, int64_t t, float (&x)[VEC]) const {
+    load_row<T, PRO>(r.at(t), li, D, x);
+  }
+  __device__ inline void zero(float (&x)[VEC]) const {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) x[i] = 0.f;
+  }
+  // Loads a q or k row and, with the prologue, normalises and rotates it.
+  __device__ inline void load_qk(const Rows<T>& r, int64_t t, const float* w, float (&x)[VEC]) const {
+    load(r, t, x);
+    if constexpr (PRO) {
+      float c[PL::HV], s[PL::HV];
+      PL::load_cs(rc, rs, t, li, D, c, s);
+      PL::forward(x, w, c, s, li, D, eps);
+    }
+  }
+  __device__ inline float dot(const float (&a)[VEC], const float (&b)[VEC]) const {
+    return row_sum<LPR>(dot_partial<VEC>(a, b));
+  }
+};
+
+// Weights and score gradients of one query from its sources.
+template <int NS, int VEC, int LPR>
+__device__ inline void query_grads(const float (&q)[VEC], const float (&go)[VEC], float lse,
+                                   float scale, const float* const (&ks)[NS],
+                                   const float* const (&vs)[NS], const bool (&ok)[NS],
+                                   float (&pp)[NS], float (&ds)[NS]) {
+  float dp[NS];
+  float delta = 0.f;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    float a = 0.f, d = 0.f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      a = __builtin_fmaf(q[e], ks[s][e], a);
+      d = __builtin_fmaf(go[e], vs[s][e], d);
+    }
+    a = row_sum<LPR>(a) * scale;
+    d = row_sum<LPR>(d);
+    pp[s] = ok[s] ? fast_exp(a - lse) : 0.f;
+    dp[s] = d;
+    delta = __builtin_fmaf(pp[s], d, delta);
+  }
+#pragma unroll
+  for (int s = 0; s < NS; ++s) ds[s] = pp[s] * (dp[s] - delta);
+}
+
+template <int NM>
+struct NearSet {
+  static constexpr bool has0 = NM & 1, has1 = NM & 2, has2 = NM & 4;
+  static constexpr int count = (int)has0 + (int)has1 + (int)has2;
+  // n-th near offset present (0 <= idx < count).
+  static constexpr int off(int idx) {
+    int seen = 0;
+    for (int o = 0; o < 3; ++o)
+      if (NM & (1 << o)) {
+        if (seen == idx) return o;
+        ++seen;
+      }
+    return -1;
+  }
+};
+
+// =================================================================== forward
+
+template <typename T, int LPR, int NM, bool FAR, bool PRO>
+struct FwdWalker {
+  static constexpr int VEC = VecOf<T>::value;
+  static constexpr int NN = NearSet<NM>::count;
+  static constexpr int NS = NN + (FAR ? 1 : 0);
+  using L = Lane<T, LPR, PRO>;
+
+  L ln;
+  Rows<T> q, k, v;
+  T* __restrict__ o;
+  int64_t ost;
+  float* __restrict__ lse;
+  float scale;
+  int F;
+  float kr[3][VEC], vr[3][VEC];
+
+  template <int R>
+  __device__ inline void step(int t) {
+    ln.load_qk(k, t, ln.wk, kr[R]);
+    ln.load(v, t, vr[R]);
+    float qr[VEC];
+    ln.load_qk(q, t, ln.wq, qr);
+    const int tf = t - F;
+    float kf[VEC], vf[VEC];
+    if constexpr (FAR) {
+      if (tf >= 0) {
+        ln.load_qk(k, tf, ln.wk, kf);
+        ln.load(v, tf, vf);
+      } else {
+        ln.zero(kf);
+        ln.zero(vf);
+      }
+    }
+    float sc[NS];
+    bool ok[NS];
+    const float* vs[NS];
+    int idx = 0;
+#pragma unroll
+    for (int n = 0; n < 3; ++n) {
+      if (NM & (1 << n)) {
+        const int slot = (R + 3 - n) % 3;
+        ok[idx] = t - n >= 0;
+        sc[idx] = ln.dot(qr, kr[slot]) * scale;
+        vs[idx] = vr[slot];
+        ++idx;
+      }
+    }
+    if constexpr (FAR) {
+      ok[NS - 1] = tf >= 0;
+      sc[NS - 1] = ln.dot(qr, kf) * scale;
+      vs[NS - 1] = vf;
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      if (ok[s]) m = fmaxf(m, sc[s]);
+    float acc[VEC];
+    ln.zero(acc);
+    float l = 0.f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const float w = ok[s] ? fast_exp(sc[s] - m) : 0.f;
+      l += w;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[e] = __builtin_fmaf(w, vs[s][e], acc[e]);
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] *= inv;
+    store_row<T, PRO>(o + (int64_t)t * ost, ln.li, ln.D, acc);
+    if (ln.li == 0) lse[t] = l > 0.f ? m + fast_log(l) : INFINITY;
+  }
+
+  // Loads position t's k/v into rotation slot R (zeros before the start).
+  template <int R>
+  __device__ inline void prefill(int t) {
+    if (t >= 0) {
+      ln.load_qk(k, t, ln.wk, kr[R]);
+      ln.load(v, t, vr[R]);
+    } else {
+      ln.zero(kr[R]);
+      ln.zero(vr[R]);
+    }
+  }
+};
+
+template <typename T, int LPR, int NM, bool FAR, bool PRO>
+__global__ __launch_bounds__(kWalkBlock) void fwd_walk(Params p, WalkCfg c) {
+  int b, hg, a;
+  if (!decode_tile(p, c, wave_id(), b, hg, a)) return;
+  const int lane = threadIdx.x & 63;
+  const int h = hg * (64 / LPR) + lane / LPR;
+  FwdWalker<T, LPR, NM, FAR, PRO> w;
+  w.ln.init(p, lane % LPR);
+  w.q = {reinterpret_cast<const T*>(p.q.p) + (int64_t)b * p.q.sb + (int64_t)h * p.q.sh, p.q.st};
+  w.k = {reinterpret_cast<const T*>(p.k.p) + (int64_t)b * p.k.sb + (int64_t)h * p.k.sh, p.k.st};
+  w.v = {reinterpret_cast<const T*>(p.v.p) + (int64_t)b * p.v.sb + (int64_t)h * p.v.sh, p.v.st};
+  w.o = reinterpret_cast<T*>(p.o.p) + (int64_t)b * p.o.sb + (int64_t)h * p.o.sh;
+  w.ost = p.o.st;
+  w.lse = p.lse + ((int64_t)b * p.H + h) * p.T;
+  w.scale = p.scale;
+  w.F = c.F;
+  const int end = min(a + c.P, p.T);
+  // Rotation slot of position t is (t - a) mod 3: a-1 -> 2, a-2 -> 1.
+  if constexpr ((NM & 6) != 0) {
+    w.template prefill<2>(a - 1);
+    w.template prefill<1>(a - 2);
+  }
+  int t = a;
+  for (; t + 3 <= end; t += 3) {
+    w.template step<0>(t);
+    w.template step<1>(t + 1);
+    w.template step<2>(t + 2);
+  }
+  if (t < end) w.template step<0>(t);
+  if (t + 1 < end) w.template step<1>(t + 1);
+}
+
+// ================================================================== backward
+
+template <typename T, int LPR, int NM, bool FAR, bool PRO>
+struct BwdWalker {
+  static constexpr int VEC = VecOf<T>::value;
+  static constexpr int NN = NearSet<NM>::count;
+  static constexpr int NS = NN + (FAR ? 1 : 0);
+  using L = Lane<T, LPR, PRO>;
+  using PL = Prologue<T, LPR>;
+
+  L ln;
+  Rows<T> q, k, v, go;
+  T* __restrict__ dq;
+  T* __restrict__ dk;
+  T* __restrict__ dv;
+  int64_t dqst, dkst, dvst;
+  const float* __restrict__ lse;
+  float scale;
+  int F, T_, a, end, qend;
+  float kr[3][VEC], vr[3][VEC];     // own rotation: k, v at u (slot R), u-1, u-2
+  float fk[3][VEC], fv[3][VEC];     // far-right rotation: i = u-2+F, i-1, i-2
+  float ak[3][VEC], av[3][VEC];     // key accumulators: keys u, u-1, u-2
+  float dwq[VEC], dwk[VEC];         // prologue weight-gradient partials
+
+  template <int R>
+  __device__ inline void step(int u) {
+    constexpr int R1 = (R + 2) % 3;   // slot of u-1
+    constexpr int R2 = (R + 1) % 3;   // slot of u-2
+    // 1. Own rotation push and fresh accumulator for key u.
+    if (u >= 0 && u < T_) {
+      ln.load_qk(k, u, ln.wk, kr[R]);
+      ln.load(v, u, vr[R]);
+    } else {
+      ln.zero(kr[R]);
+      ln.zero(vr[R]);
+    }
+    ln.zero(ak[R]);
+    ln.zero(av[R]);
+    // 2. Far-right rotation push: position u - 2 + F.
+    if constexpr (FAR) {
+      const int i = u - 2 + F;
+      if (i >= 0 && i < T_) {
+        ln.load_qk(k, i, ln.wk, fk[R]);
+        ln.load(v, i, fv[R]);
+      } else {
+        ln.zero(fk[R]);
+        ln.zero(fv[R]);
+      }
+    }
+    // 3. Own query u.
+    if (u >= a && u < qend) {
+      float qr[VEC], gr[VEC], xq[VEC];
+      float rq = 0.f, cq[PL::HV], sq[PL::HV];
+      ln.load(q, u, xq);
+      if constexpr (PRO) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) qr[e] = xq[e];
+        PL::load_cs(ln.rc, ln.rs, u, ln.li, ln.D, cq, sq);
+        rq = PL::forward(qr, ln.wq, cq, sq, ln.li, ln.D, ln.eps);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) qr[e] = xq[e];
+      }
+      ln.load(go, u, gr);
+      const float l = lse[u];
+      float kf[VEC], vf[VEC];
+      const int uf = u - F;
+      if constexpr (FAR) {
+        if (uf >= 0) {
+          ln.load_qk(k, uf, ln.wk, kf);
+          ln.load(v, uf, vf);
+        } else {
+          ln.zero(kf);
+          ln.zero(vf);
+        }
+      }
+      const float* ks[NS];
+      const float* vs[NS];
+      bool ok[NS];
+      int idx = 0;
+#pragma unroll
+      for (int n = 0; n < 3; ++n) {
+        if (NM & (1 << n)) {
+          const int slot = (R + 3 - n) % 3;
+          ks[idx] = kr[slot];
+          vs[idx] = vr[slot];
+          ok[idx] = u - n >= 0;
+          ++idx;
+        }
+      }
+      if constexpr (FAR) {
+        ks[NS - 1] = kf;
+        vs[NS - 1] = vf;
+        ok[NS - 1] = uf >= 0;
+      }
+      float pp[NS], ds[NS];
+      query_grads<NS, VEC, LPR>(qr, gr, l, scale, ks, vs, ok, pp, ds);
+      if (u < end) {
+        float g[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          float acc = 0.f;
+#pragma unroll
+          for (int s = 0; s < NS; ++s) acc = __builtin_fmaf(ds[s], ks[s][e], acc);
+          g[e] = acc * scale;
+        }
+        if constexpr (PRO) PL::backward(g, xq, rq, ln.wq, cq, sq, ln.li, ln.D, dwq);
+        store_row<T, PRO>(dq + (int64_t)u * dqst, ln.li, ln.D, g);
+      }
+      // Near-slot contributions to keys u - n.
+      idx = 0;
+#pragma unroll
+      for (int n = 0; n < 3; ++n) {
+        if (NM & (1 << n)) {
+          const int slot = (R + 3 - n) % 3;
+          const float cs = ds[idx] * scale, cp = pp[idx];
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            ak[slot][e] = __builtin_fmaf(cs, qr[e], ak[slot][e]);
+            av[slot][e] = __builtin_fmaf(cp, gr[e], av[slot][e]);
+          }
+          ++idx;
+        }
+      }
+    }
+    // 4. Key j = u - 2 is complete but for its far query i = j + F.
+    const int j = u - 2;
+    if (j >= a && j < end) {
+      if constexpr (FAR) {
+        const int i = j + F;
+        if (i < T_) {
+          float qr[VEC], gr[VEC];
+          ln.load_qk(q, i, ln.wq, qr);
+          ln.load(go, i, gr);
+          const float l = lse[i];
+          const float* ks[NS];
+          const float* vs[NS];
+          bool ok[NS];
+          int idx = 0;
+#pragma unroll
+          for (int n = 0; n < 3; ++n) {
+            if (NM & (1 << n)) {
+              const int slot = (R + 3 - n) % 3;
+              ks[idx] = fk[slot];
+              vs[idx] = fv[slot];
+              ok[idx] = true;   // i - n >= F - 2 > 0
+              ++idx;
+            }
+          }
+          ks[NS - 1] = kr[R2];
+          vs[NS - 1] = vr[R2];
+          ok[NS - 1] = true;
+          float pp[NS], ds[NS];
+          query_grads<NS, VEC, LPR>(qr, gr, l, scale, ks, vs, ok, pp, ds);
+          const float cs = ds[NS - 1] * scale, cp = pp[NS - 1];
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            ak[R2][e] = __builtin_fmaf(cs, qr[e], ak[R2][e]);
+            av[R2][e] = __builtin_fmaf(cp, gr[e], av[R2][e]);
+          }
+        }
+      }
+      if constexpr (PRO) {
+        float xk[VEC], c[PL::HV], s[PL::HV];
+        ln.load(k, j, xk);
+        PL::load_cs(ln.rc, ln.rs, j, ln.li, ln.D, c, s);
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) ss = __builtin_fmaf(xk[e], xk[e], ss);
+        ss = row_sum<LPR>(ss);
+        const float r = __builtin_amdgcn_rsqf(__fadd_rn(__fdiv_rn(ss, (float)ln.D), ln.eps));
+        PL::backward(ak[R2], xk, r, ln.wk, c, s, ln.li, ln.D, dwk);
+      }
+      store_row<T, PRO>(dk + (int64_t)j * dkst, ln.li, ln.D, ak[R2]);
+      store_row<T, PRO>(dv + (int64_t)j * dvst, ln.li, ln.D, av[R2]);
+    }
+    (void)R1;
+  }
+};
+
+// Sums a per-lane weight-gradient partial over the wave's heads and writes
+// it as row `wave` of `part` (fixed butterfly order: deterministic).
+template <typename T, int LPR, bool SPLIT>
+__device__ inline void write_wave_partial(float (&x)[VecOf<T>::value], float* part, int64_t wave,
+                                          int D) {
+  constexpr int VEC = VecOf<T>::value;
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+#pragma unroll
+    for (int m = LPR; m < 64; m <<= 1) x[e] += __shfl_xor(x[e], m, 64);
+  }
+  if (lane < LPR) {
+    float* row = part + wave * D;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const int d = elem_index<T, SPLIT>(lane, e, D);
+      if (SPLIT ? (lane * (VEC / 2) < (D >> 1)) : (lane * VEC < D)) row[d] = x[e];
+    }
+  }
+}
+
+template <typename T, int LPR, int NM, bool FAR, bool PRO>
+__global__ __launch_bounds__(kWalkBlock) void bwd_walk(Params p, WalkCfg c) {
+  constexpr int VEC = VecOf<T>::value;
+  const int64_t wave = wave_id();
+  int b, hg, a;
+  const bool live = decode_tile(p, c, wave, b, hg, a);
+  const int lane = threadIdx.x & 63;
+  BwdWalker<T, LPR, NM, FAR, PRO> w;
+  w.ln.zero(w.dwq);
+  w.ln.zero(w.dwk);
+  if (live) {
+    const int h = hg * (64 / LPR) + lane / LPR;
+    w.ln.init(p, lane % LPR);
+    auto rows = [&](const View& vw) {
+      return Rows<T>{reinterpret_cast<const T*>(vw.p) + (int64_t)b * vw.sb + (int64_t)h * vw.sh, vw.st};
+    };
+    w.q = rows(p.q);
+    w.k = rows(p.k);
+    w.v = rows(p.v);
+    w.go = rows(p.dout);
+    w.dq = reinterpret_cast<T*>(p.dq.p) + (int64_t)b * p.dq.sb + (int64_t)h * p.dq.sh;
+    w.dk = reinterpret_cast<T*>(p.dk.p) + (int64_t)b * p.dk.sb + (int64_t)h * p.dk.sh;
+    w.dv = reinterpret_cast<T*>(p.dv.p) + (int64_t)b * p.dv.sb + (int64_t)h * p.dv.sh;
+    w.dqst = p.dq.st;
+    w.dkst = p.dk.st;
+    w.dvst = p.dv.st;
+    w.lse = p.lse + ((int64_t)b * p.H + h) * p.T;
+    w.scale = p.scale;
+    w.F = c.F;
+    w.T_ = p.T;
+    w.a = a;
+    w.end = min(a + c.P, p.T);
+    w.qend = min(w.end + 2, p.T);
+    // Walk u = a-2 .. end+1; rotation slot of u is (u - a + 2) mod 3.
+    const int last = w.end + 1;
+    int u = a - 2;
+    for (; u + 3 <= last + 1; u += 3) {
+      w.template step<0>(u);
+      w.template step<1>(u + 1);
+      w.template step<2>(u + 2);
+    }
+    if (u <= last) w.template step<0>(u);
+    if (u + 1 <= last) w.template step<1>(u + 1);
+  }
+  if constexpr (PRO) {
+    write_wave_partial<T, LPR, true>(w.dwq, p.dwq_part, wave, p.D);
+    write_wave_partial<T, LPR, true>(w.dwk, p.dwk_part, wave, p.D);
+  }
+  (void)VEC;
+}
+
+// ================================================================= dispatch
+
+struct Pattern {
+  int nm;     // near mask over offsets {0, 1, 2}
+  int far;    // far offset (0 if none)
+};
+
+// Classifies offsets: each distinct, at most one offset >= 3.
+bool classify(const Params& p, Pattern* out) {
+  int nm = 0, far = 0, nfar = 0;
+  for (int s = 0; s < p.S; ++s) {
+    const int o = p.off[s];
+    for (int r = 0; r < s; ++r)
+      if (p.off[r] == o) return false;
+    if (o <= 2) {
+      nm |= 1 << o;
+    } else {
+      far = o;
+      ++nfar;
+    }
+  }
+  if (nfar > 1) return false;
+  // Supported patterns: (0,1), (0,2), (0,1,2,F), (0,F).
+  const bool ok = (nfar == 0 && (nm == 3 || nm == 5)) || (nfar == 1 && (nm == 7 || nm == 1));
+  if (!ok) return false;
+  out->nm = nm;
+  out->far = far;
+  return true;
+}
+
+int walk_lpr(const Params& p, int dtype) {
+  const int esz = dtype == kFP32 ? 4 : 2;
+  if ((p.D * esz) % 16) return 0;
+  const int lpr = p.D * esz / 16;
+  if (lpr != 4 && lpr != 8 && lpr != 16) return 0;
+  return lpr;
+}
+
+WalkCfg make_cfg(const Params& p, int lpr, const Pattern& pat) {
+  WalkCfg c{};
+  c.HG = p.H / (64 / lpr);
+  const int64_t lanes_rows = (int64_t)p.B * c.HG;
+  // About 8192 tiles fill 256 CUs several times over; the tile is at least
+  // 16 positions (halo overhead <= 2/16) and at most 256.
+  int P = 256;
+  while (P > 16 && lanes_rows * ((p.T + P - 1) / P) < 8192) P >>= 1;
+  c.P = P;
+  c.F = pat.far;
+  if (pat.far >= P && pat.far % P == 0) {
+    c.column = 1;
+    c.rows = (p.T + pat.far - 1) / pat.far;
+    c.tiles_t = c.rows * (pat.far / P);
+  } else {
+    c.column = 0;
+    c.rows = 0;
+    c.tiles_t = (p.T + P - 1) / P;
+  }
+  c.total = lanes_rows * c.tiles_t;
+  c.nwg = (int)((c.total + kWaves - 1) / kWaves);
+  return c;
+}
+
+template <typename T, int LPR, bool PRO, bool FWD>
+hipError_t launch_pattern(const Params& p, const WalkCfg& c, const Pattern& pat, hipStream_t st) {
+  const dim3 grid((unsigned)c.nwg), block(kWalkBlock);
+#define SBDA_WALK_CASE(NMV, FARV)                                                            \
+  if (pat.nm == NMV && (pat.far != 0) == FARV) {                                             \
+    if (FWD)                                                                                 \
+      hipLaunchKernelGGL((fwd_walk<T, LPR, NMV, FARV, PRO>), grid, block, 0, st, p, c);     \
+    else                                                                                     \
+      hipLaunchKernelGGL((bwd_walk<T, LPR, NMV, FARV, PRO>), grid, block, 0, st, p, c);     \
+    return hipGetLastError();                                                                \
+  }
+  SBDA_WALK_CASE(3, false)
+  SBDA_WALK_CASE(5, false)
+  SBDA_WALK_CASE(7, true)
+  SBDA_WALK_CASE(1, true)
+#undef SBDA_WALK_CASE
+  return hipErrorInvalidValue;
+}
+
+template <typename T>
+struct TypeTag {
+  using type = T;
+};
+
+template <bool FWD>
+hipError_t walk_launch(const Params& p, int dtype, bool pro, hipStream_t st) {
+  Pattern pat;
+  if (!classify(p, &pat)) return hipErrorInvalidValue;
+  const int lpr = walk_lpr(p, dtype);
+  const WalkCfg c = make_cfg(p, lpr, pat);
+  auto go = [&](auto tag, auto lprc) -> hipError_t {
+    using T = typename decltype(tag)::type;
+    constexpr int L = decltype(lprc)::value;
+    return pro ? launch_pattern<T, L, true, FWD>(p, c, pat, st)
+               : launch_pattern<T, L, false, FWD>(p, c, pat, st);
+  };
+  auto by_lpr = [&](auto tag) -> hipError_t {
+    switch (lpr) {
+      case 4: return go(tag, std::integral_constant<int, 4>{});
+      case 8: return go(tag, std::integral_constant<int, 8>{});
+      case 16: return go(tag, std::integral_constant<int, 16>{});
+      default: return hipErrorInvalidValue;
+    }
+  };
+  switch (dtype) {
+    case kBF16: return by_lpr(TypeTag<__bf16>{});
+    case kFP16: return by_lpr(TypeTag<_Float16>{});
+    case kFP32: return by_lpr(TypeTag<float>{});
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+bool walk_applies(const Params& p, int dtype) {
+  Pattern pat;
+  if (p.group != 1 || !classify(p, &pat)) return false;
+  const int lpr = walk_lpr(p, dtype);
+  if (lpr == 0) return false;
+  return p.H % (64 / lpr) == 0;
+}
+
+hipError_t walk_forward(const Params& p, int dtype, bool pro, hipStream_t st) {
+  return walk_launch<true>(p, dtype, pro, st);
+}
+
+hipError_t walk_backward(const Params& p, int dtype, bool pro, hipStream_t st) {
+  return walk_launch<false>(p, dtype, pro, st);
+}
+
+void walk_partials(const Params& p, int dtype, int64_t* pq, int64_t* pk) {
+  Pattern pat;
+  classify(p, &pat);
+  const WalkCfg c = make_cfg(p, walk_lpr(p, dtype), pat);
+  *pq = (int64_t)c.nwg * kWaves;
+  *pk = *pq;
+}
 
 }  // namespace sbda

@@ -291,3 +291,16 @@ def test_rope_table_matches_fp32_reference_angles():
         want_c, want_s = ref.rope_tables(t, d, theta, torch.float32)
         torch.testing.assert_close(cos.cpu(), want_c[:, : d // 2], rtol=0, atol=3e-7)
         torch.testing.assert_close(sin.cpu(), want_s[:, : d // 2], rtol=0, atol=3e-7)
+
+
+@pytest.mark.parametrize("t", [1, 2, 3, 5, 17, 300, 3000])
+@pytest.mark.parametrize("offs", [(0, 1), (0, 2), (0, 1, 2, 3), (0, 1, 2, 16), (0, 1, 2, 1024),
+                                  (0, 4), (2, 0, 1, 64)])
+def test_tile_edges_and_offset_patterns(t, offs):
+    # Lengths that are not multiples of the tile, the 3-step unroll or the far
+    # offset; far offsets below, at and above the tile size (linear and
+    # column tile orders); near-only, near+far and far-only patterns.
+    q, k, v, g = _inputs(2, t, 8, 64, torch.bfloat16, seed=t * 31 + sum(offs))
+    _close(_fused(q, k, v, offs, g), _oracle(q, k, v, offs, g), LOW_TOL, f"T={t} {offs}")
+    q, k, v, g = _inputs(1, t, 8, 64, torch.float32, seed=t * 37 + sum(offs))
+    _close(_fused(q, k, v, offs, g), _oracle(q, k, v, offs, g), FP32_TOL, f"fp32 T={t} {offs}")

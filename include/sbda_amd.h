@@ -60,7 +60,8 @@ const char* sbda_last_error(void);
 /*
  * Forward.  q: [B,H,T,D]; k, v: [B,Hkv,T,D] (H % Hkv == 0, query head h reads
  * kv head h / (H/Hkv)).  Writes out ([B,H,T,D], any strides as above) and
- * lse ([B,H,T] fp32 contiguous; +inf marks a row with no valid source).
+ * lse: one fp32 log-normaliser per row, stored [B,T,H] contiguous (position
+ * major, like q/k/v memory); +inf marks a row with no valid source.
  * Scale is head_dim**-0.5 in fp32.
  */
 int sbda_forward(const void* q, const int64_t* q_strides,

@@ -11,7 +11,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("libsbda_amd.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 OK, ERR_VALUE, ERR_DTYPE, ERR_RUNTIME = 0, 1, 2, 3
 _ERRORS = {ERR_VALUE: ValueError, ERR_DTYPE: TypeError, ERR_RUNTIME: RuntimeError}

@@ -202,7 +202,7 @@ using namespace sbda;
 
 extern "C" {
 
-int sbda_abi_version(void) { return 2; }
+int sbda_abi_version(void) { return 3; }
 
 const char* sbda_last_error(void) { return g_error.c_str(); }
 

@@ -144,11 +144,26 @@ __device__ inline int elem_index(int li, int i, int D) {
   }
 }
 
-// Butterfly sum over the LPR lanes of one row (fixed order: deterministic).
+// Cross-lane move within a 16-lane DPP row (CTRL is the dpp_ctrl encoding).
+template <int CTRL>
+__device__ inline float dpp(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the LPR lanes of one row, every lane receiving the same bits.
+// Steps: swap neighbours (quad_perm 1,0,3,2), swap pairs (quad_perm
+// 2,3,0,1), mirror within 8 lanes, mirror within 16 lanes; each step adds
+// two values that the partner lane adds in the other order, so all lanes
+// agree exactly.  Groups wider than a DPP row finish with lane shuffles.
 template <int LPR>
 __device__ inline float row_sum(float x) {
+  if constexpr (LPR >= 2) x += dpp<0xB1>(x);
+  if constexpr (LPR >= 4) x += dpp<0x4E>(x);
+  if constexpr (LPR >= 8) x += dpp<0x141>(x);
+  if constexpr (LPR >= 16) x += dpp<0x140>(x);
 #pragma unroll
-  for (int m = 1; m < LPR; m <<= 1) x += __shfl_xor(x, m, 64);
+  for (int m = 16; m < LPR; m <<= 1) x += __shfl_xor(x, m, 64);
   return x;
 }
 

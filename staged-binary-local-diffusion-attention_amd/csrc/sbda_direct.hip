@@ -143,7 +143,7 @@ __global__ __launch_bounds__(kBlock) void fwd_direct(Params p) {
   for (int i = 0; i < VEC; ++i) acc[i] *= inv;
   if (live) {
     store_row<T, PRO>(row_ptr<T>(p.o, b, h, t), li, p.D, acc);
-    if (li == 0) p.lse[((int64_t)b * p.H + h) * p.T + t] = l > 0.f ? m + fast_log(l) : INFINITY;
+    if (li == 0) p.lse[((int64_t)b * p.T + t) * p.H + h] = l > 0.f ? m + fast_log(l) : INFINITY;
   }
 }
 
@@ -166,7 +166,7 @@ __device__ inline void query_side(const Params& p, int b, int i, int h, int hk, 
     PL::forward(q, p.wq, c, s, li, p.D, p.eps);
   }
   load_row<T, PRO>(row_ptr<T>(p.dout, b, h, i), li, p.D, go);
-  const float lse = p.lse[((int64_t)b * p.H + h) * p.T + i];
+  const float lse = p.lse[((int64_t)b * p.T + i) * p.H + h];
   float dp[kMaxSlots];
   float delta = 0.f;
 #pragma unroll

@@ -22,7 +22,7 @@ constexpr int kMaxSlots = 4;
 struct Params {
   View q, k, v, dout;          // q and k are the raw (pre-prologue) rows when the prologue is fused
   MutView o, dq, dk, dv;
-  float* lse;                  // [B, H, T] fp32, contiguous
+  float* lse;                  // [B, T, H] fp32, contiguous
   int B, H, Hkv, group, T, D, S;
   int off[kMaxSlots];
   float scale;

@@ -181,6 +181,7 @@ struct FwdWalker {
   T* __restrict__ o;
   int64_t ost;
   float* __restrict__ lse;
+  int lst;
   float scale;
   int F;
   float kr[3][VEC], vr[3][VEC];
@@ -239,7 +240,7 @@ struct FwdWalker {
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[e] *= inv;
     store_row<T, PRO>(o + (int64_t)t * ost, ln.li, ln.D, acc);
-    if (ln.li == 0) lse[t] = l > 0.f ? m + fast_log(l) : INFINITY;
+    if (ln.li == 0) lse[(int64_t)t * lst] = l > 0.f ? m + fast_log(l) : INFINITY;
   }
 
   // Loads position t's k/v into rotation slot R (zeros before the start).
@@ -268,7 +269,8 @@ __global__ __launch_bounds__(kWalkBlock) void fwd_walk(Params p, WalkCfg c) {
   w.v = {reinterpret_cast<const T*>(p.v.p) + (int64_t)b * p.v.sb + (int64_t)h * p.v.sh, p.v.st};
   w.o = reinterpret_cast<T*>(p.o.p) + (int64_t)b * p.o.sb + (int64_t)h * p.o.sh;
   w.ost = p.o.st;
-  w.lse = p.lse + ((int64_t)b * p.H + h) * p.T;
+  w.lse = p.lse + (int64_t)b * p.T * p.H + h;
+  w.lst = p.H;
   w.scale = p.scale;
   w.F = c.F;
   const int end = min(a + c.P, p.T);
@@ -304,6 +306,7 @@ struct BwdWalker {
   T* __restrict__ dv;
   int64_t dqst, dkst, dvst;
   const float* __restrict__ lse;
+  int lst;
   float scale;
   int F, T_, a, end, qend;
   float kr[3][VEC], vr[3][VEC];     // own rotation: k, v at u (slot R), u-1, u-2
@@ -351,7 +354,7 @@ struct BwdWalker {
         for (int e = 0; e < VEC; ++e) qr[e] = xq[e];
       }
       ln.load(go, u, gr);
-      const float l = lse[u];
+      const float l = lse[(int64_t)u * lst];
       float kf[VEC], vf[VEC];
       const int uf = u - F;
       if constexpr (FAR) {
@@ -421,7 +424,7 @@ struct BwdWalker {
           float qr[VEC], gr[VEC];
           ln.load_qk(q, i, ln.wq, qr);
           ln.load(go, i, gr);
-          const float l = lse[i];
+          const float l = lse[(int64_t)i * lst];
           const float* ks[NS];
           const float* vs[NS];
           bool ok[NS];
@@ -515,7 +518,8 @@ __global__ __launch_bounds__(kWalkBlock) void bwd_walk(Params p, WalkCfg c) {
     w.dqst = p.dq.st;
     w.dkst = p.dk.st;
     w.dvst = p.dv.st;
-    w.lse = p.lse + ((int64_t)b * p.H + h) * p.T;
+    w.lse = p.lse + (int64_t)b * p.T * p.H + h;
+  w.lst = p.H;
     w.scale = p.scale;
     w.F = c.F;
     w.T_ = p.T;
@@ -538,6 +542,405 @@ __global__ __launch_bounds__(kWalkBlock) void bwd_walk(Params p, WalkCfg c) {
     write_wave_partial<T, LPR, true>(w.dwk, p.dwk_part, wave, p.D);
   }
   (void)VEC;
+}
+
+// ========================================================= pipelined walks
+//
+// The same walks without the prologue, software-pipelined: while step u is
+// computed, every row step u+1 needs is already in flight.  Loads are
+// unconditional (positions clamped into [0, T), validity applied as masks)
+// so the compiler can keep them outstanding across steps.  Rows stay in
+// their 16-byte raw form; dot products use v_dot2_f32_{bf16,f16} on the raw
+// pairs and rows are widened to fp32 only where they are accumulated.
+// Rotation depth 4 (positions u+1 .. u-2) with the loop unrolled by 4.
+
+struct Raw {
+  uint32_t w[4];
+};
+
+template <typename T>
+__device__ inline Raw load_raw(const T* __restrict__ row, int li) {
+  const uint4 x = *reinterpret_cast<const uint4*>(row + li * VecOf<T>::value);
+  return Raw{{x.x, x.y, x.z, x.w}};
+}
+
+template <typename T>
+__device__ inline void widen(const Raw& r, float (&x)[VecOf<T>::value]) {
+  unpack_words<T, 4>(r.w, x);
+}
+
+template <typename T>
+__device__ inline float dot_raw(const Raw& a, const Raw& b) {
+  float s = 0.f;
+  if constexpr (std::is_same<T, __bf16>::value) {
+    typedef __attribute__((ext_vector_type(2))) __bf16 bf2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.w[i]),
+                                          __builtin_bit_cast(bf2, b.w[i]), s, false);
+  } else if constexpr (std::is_same<T, _Float16>::value) {
+    typedef __attribute__((ext_vector_type(2))) _Float16 h2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      s = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a.w[i]), __builtin_bit_cast(h2, b.w[i]),
+                                 s, false);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s = __builtin_fmaf(__uint_as_float(a.w[i]), __uint_as_float(b.w[i]), s);
+  }
+  return s;
+}
+
+__device__ inline int clampi(int x, int hi) { return x < 0 ? 0 : (x > hi ? hi : x); }
+
+template <typename T, int LPR, int NM, bool FAR>
+struct FwdPipe {
+  static constexpr int VEC = VecOf<T>::value;
+  static constexpr int NN = NearSet<NM>::count;
+  static constexpr int NS = NN + (FAR ? 1 : 0);
+
+  const T* __restrict__ q;
+  const T* __restrict__ k;
+  const T* __restrict__ v;
+  T* __restrict__ o;
+  float* __restrict__ lse;
+  int lst;
+  int64_t qst, kst, vst, ost;
+  float scale;
+  int F, Tm1, li;
+  Raw kr[4];            // k at t (slot R), t-1, t-2; slot R+1 is being fetched
+  Raw vraw[2], qn[2];   // this step's v and q (stage R & 1)
+  Raw kl[2], vl[2];     // far source t - F
+  float vr[4][VEC];     // widened v rotation
+
+  template <int R>
+  __device__ inline void prefetch(int t) {
+    const int tc = clampi(t, Tm1);
+    kr[R] = load_raw<T>(k + (int64_t)tc * kst, li);
+    vraw[R & 1] = load_raw<T>(v + (int64_t)tc * vst, li);
+    qn[R & 1] = load_raw<T>(q + (int64_t)tc * qst, li);
+    if constexpr (FAR) {
+      const int tf = clampi(t - F, Tm1);
+      kl[R & 1] = load_raw<T>(k + (int64_t)tf * kst, li);
+      vl[R & 1] = load_raw<T>(v + (int64_t)tf * vst, li);
+    }
+  }
+
+  template <int R>
+  __device__ inline void compute(int t, bool store) {
+    widen<T>(vraw[R & 1], vr[R]);
+    float sc[NS];
+    bool ok[NS];
+    int idx = 0;
+#pragma unroll
+    for (int n = 0; n < 3; ++n) {
+      if (NM & (1 << n)) {
+        ok[idx] = t - n >= 0;
+        sc[idx] = row_sum<LPR>(dot_raw<T>(qn[R & 1], kr[(R + 4 - n) & 3])) * scale;
+        ++idx;
+      }
+    }
+    float vf[VEC];
+    if constexpr (FAR) {
+      ok[NS - 1] = t - F >= 0;
+      sc[NS - 1] = row_sum<LPR>(dot_raw<T>(qn[R & 1], kl[R & 1])) * scale;
+      widen<T>(vl[R & 1], vf);
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) m = ok[s] ? fmaxf(m, sc[s]) : m;
+    float w[NS], l = 0.f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      w[s] = ok[s] ? fast_exp(sc[s] - m) : 0.f;
+      l += w[s];
+    }
+    float acc[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+    idx = 0;
+#pragma unroll
+    for (int n = 0; n < 3; ++n) {
+      if (NM & (1 << n)) {
+        const int slot = (R + 4 - n) & 3;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] = __builtin_fmaf(w[idx], vr[slot][e], acc[e]);
+        ++idx;
+      }
+    }
+    if constexpr (FAR) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[e] = __builtin_fmaf(w[NS - 1], vf[e], acc[e]);
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] *= inv;
+    if (store) {
+      store_row<T, false>(o + (int64_t)t * ost, li, VEC * LPR, acc);
+      if (li == 0) lse[(int64_t)t * lst] = l > 0.f ? m + fast_log(l) : INFINITY;
+    }
+  }
+};
+
+template <typename T, int LPR, int NM, bool FAR>
+__global__ __launch_bounds__(kWalkBlock) void fwd_pipe(Params p, WalkCfg c) {
+  int b, hg, a;
+  if (!decode_tile(p, c, wave_id(), b, hg, a)) return;
+  const int lane = threadIdx.x & 63;
+  const int h = hg * (64 / LPR) + lane / LPR;
+  FwdPipe<T, LPR, NM, FAR> w;
+  w.li = lane % LPR;
+  w.q = reinterpret_cast<const T*>(p.q.p) + (int64_t)b * p.q.sb + (int64_t)h * p.q.sh;
+  w.k = reinterpret_cast<const T*>(p.k.p) + (int64_t)b * p.k.sb + (int64_t)h * p.k.sh;
+  w.v = reinterpret_cast<const T*>(p.v.p) + (int64_t)b * p.v.sb + (int64_t)h * p.v.sh;
+  w.o = reinterpret_cast<T*>(p.o.p) + (int64_t)b * p.o.sb + (int64_t)h * p.o.sh;
+  w.qst = p.q.st;
+  w.kst = p.k.st;
+  w.vst = p.v.st;
+  w.ost = p.o.st;
+  w.lse = p.lse + (int64_t)b * p.T * p.H + h;
+  w.lst = p.H;
+  w.scale = p.scale;
+  w.F = c.F;
+  w.Tm1 = p.T - 1;
+  const int end = min(a + c.P, p.T);
+  // Slot of position t is (t - a + 2) & 3: the walk starts two positions
+  // early (a-2, a-1) to fill the near-source rotation; those steps store nothing.
+  const int t0 = a - 2;
+  w.template prefetch<0>(t0);
+  for (int t = t0; t < end; t += 4) {
+    w.template prefetch<1>(t + 1);
+    w.template compute<0>(t, t >= a && t < end);
+    w.template prefetch<2>(t + 2);
+    w.template compute<1>(t + 1, t + 1 >= a && t + 1 < end);
+    w.template prefetch<3>(t + 3);
+    w.template compute<2>(t + 2, t + 2 >= a && t + 2 < end);
+    w.template prefetch<0>(t + 4);
+    w.template compute<3>(t + 3, t + 3 >= a && t + 3 < end);
+  }
+}
+
+template <typename T, int LPR, int NM, bool FAR>
+struct BwdPipe {
+  static constexpr int VEC = VecOf<T>::value;
+  static constexpr int NN = NearSet<NM>::count;
+  static constexpr int NS = NN + (FAR ? 1 : 0);
+
+  const T* __restrict__ q;
+  const T* __restrict__ k;
+  const T* __restrict__ v;
+  const T* __restrict__ go;
+  T* __restrict__ dq;
+  T* __restrict__ dk;
+  T* __restrict__ dv;
+  const float* __restrict__ lse;
+  int lst;
+  int64_t qst, kst, vst, gst, dqst, dkst, dvst;
+  float scale;
+  int F, T_, Tm1, a, end, li;
+  Raw kr[4], vr[4];     // own k/v rotation: slot of u is R
+  Raw qr[4], gr[4];     // own q/dO rotation (key finalisation reads u-2 .. u)
+  float lr[4];
+  Raw fk[4], fv[4];     // far-right k/v rotation over i = u - 2 + F
+  Raw kl[2], vl[2];     // far-left sources of query u
+  Raw qi[2], gi[2];     // far query i of key u - 2
+  float li_[2];
+  float sp[4][3], sd[4][3];  // query u's near-slot p_n and scale * dS_n
+
+  template <int R>
+  __device__ inline void prefetch(int u) {
+    const int uc = clampi(u, Tm1);
+    kr[R] = load_raw<T>(k + (int64_t)uc * kst, li);
+    vr[R] = load_raw<T>(v + (int64_t)uc * vst, li);
+    qr[R] = load_raw<T>(q + (int64_t)uc * qst, li);
+    gr[R] = load_raw<T>(go + (int64_t)uc * gst, li);
+    lr[R] = lse[(int64_t)uc * lst];
+    if constexpr (FAR) {
+      const int ul = clampi(u - F, Tm1);
+      kl[R & 1] = load_raw<T>(k + (int64_t)ul * kst, li);
+      vl[R & 1] = load_raw<T>(v + (int64_t)ul * vst, li);
+      const int i = clampi(u - 2 + F, Tm1);
+      fk[R] = load_raw<T>(k + (int64_t)i * kst, li);
+      fv[R] = load_raw<T>(v + (int64_t)i * vst, li);
+      qi[R & 1] = load_raw<T>(q + (int64_t)i * qst, li);
+      gi[R & 1] = load_raw<T>(go + (int64_t)i * gst, li);
+      li_[R & 1] = lse[(int64_t)i * lst];
+    }
+  }
+
+  // p and dS of one query from its raw operands and sources.
+  __device__ inline void grads(const Raw& qq, const Raw& gg, float l, const Raw* const (&ks)[NS],
+                               const Raw* const (&vs)[NS], const bool (&ok)[NS], float (&pp)[NS],
+                               float (&ds)[NS]) const {
+    float dp[NS];
+    float delta = 0.f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const float sc = row_sum<LPR>(dot_raw<T>(qq, *ks[s])) * scale;
+      dp[s] = row_sum<LPR>(dot_raw<T>(gg, *vs[s]));
+      pp[s] = ok[s] ? fast_exp(sc - l) : 0.f;
+      delta = __builtin_fmaf(pp[s], dp[s], delta);
+    }
+#pragma unroll
+    for (int s = 0; s < NS; ++s) ds[s] = pp[s] * (dp[s] - delta);
+  }
+
+  template <int R>
+  __device__ inline void compute(int u) {
+    // Own query u (its operands are clamped rows outside [0, T); the results
+    // are only used for queries inside the tile's range).
+    {
+      const Raw* ks[NS];
+      const Raw* vs[NS];
+      bool ok[NS];
+      int idx = 0;
+#pragma unroll
+      for (int n = 0; n < 3; ++n) {
+        if (NM & (1 << n)) {
+          ks[idx] = &kr[(R + 4 - n) & 3];
+          vs[idx] = &vr[(R + 4 - n) & 3];
+          ok[idx] = u - n >= 0;
+          ++idx;
+        }
+      }
+      if constexpr (FAR) {
+        ks[NS - 1] = &kl[R & 1];
+        vs[NS - 1] = &vl[R & 1];
+        ok[NS - 1] = u - F >= 0;
+      }
+      float pp[NS], ds[NS];
+      grads(qr[R], gr[R], lr[R], ks, vs, ok, pp, ds);
+#pragma unroll
+      for (int n = 0; n < NN; ++n) {
+        sp[R][n] = pp[n];
+        sd[R][n] = ds[n] * scale;
+      }
+      if (u >= a && u < end) {
+        float g[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) g[e] = 0.f;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          float kx[VEC];
+          widen<T>(*ks[s], kx);
+          const float c = ds[s] * scale;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) g[e] = __builtin_fmaf(c, kx[e], g[e]);
+        }
+        store_row<T, false>(dq + (int64_t)u * dqst, li, VEC * LPR, g);
+      }
+    }
+    // Key j = u - 2: near contributions from queries j + n, far from j + F.
+    const int j = u - 2;
+    if (j >= a && j < end) {
+      float ak[VEC], av[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) { ak[e] = 0.f; av[e] = 0.f; }
+      int idx = 0;
+#pragma unroll
+      for (int n = 0; n < 3; ++n) {
+        if (NM & (1 << n)) {
+          const int slot = (R + 2 + n) & 3;   // slot of query j + n
+          const bool there = j + n < T_;
+          const float cs = there ? sd[slot][idx] : 0.f;
+          const float cp = there ? sp[slot][idx] : 0.f;
+          float qx[VEC], gx[VEC];
+          widen<T>(qr[slot], qx);
+          widen<T>(gr[slot], gx);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            ak[e] = __builtin_fmaf(cs, qx[e], ak[e]);
+            av[e] = __builtin_fmaf(cp, gx[e], av[e]);
+          }
+          ++idx;
+        }
+      }
+      if constexpr (FAR) {
+        const Raw* ks[NS];
+        const Raw* vs[NS];
+        bool ok[NS];
+        int n2 = 0;
+#pragma unroll
+        for (int n = 0; n < 3; ++n) {
+          if (NM & (1 << n)) {
+            ks[n2] = &fk[(R + 4 - n) & 3];
+            vs[n2] = &fv[(R + 4 - n) & 3];
+            ok[n2] = true;   // i - n >= F - 2 > 0
+            ++n2;
+          }
+        }
+        ks[NS - 1] = &kr[(R + 2) & 3];   // key j itself
+        vs[NS - 1] = &vr[(R + 2) & 3];
+        ok[NS - 1] = true;
+        float pp[NS], ds[NS];
+        grads(qi[R & 1], gi[R & 1], li_[R & 1], ks, vs, ok, pp, ds);
+        const bool there = j + F < T_;
+        const float cs = there ? ds[NS - 1] * scale : 0.f;
+        const float cp = there ? pp[NS - 1] : 0.f;
+        float qx[VEC], gx[VEC];
+        widen<T>(qi[R & 1], qx);
+        widen<T>(gi[R & 1], gx);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          ak[e] = __builtin_fmaf(cs, qx[e], ak[e]);
+          av[e] = __builtin_fmaf(cp, gx[e], av[e]);
+        }
+      }
+      store_row<T, false>(dk + (int64_t)j * dkst, li, VEC * LPR, ak);
+      store_row<T, false>(dv + (int64_t)j * dvst, li, VEC * LPR, av);
+    }
+  }
+};
+
+template <typename T, int LPR, int NM, bool FAR>
+__global__ __launch_bounds__(kWalkBlock) void bwd_pipe(Params p, WalkCfg c) {
+  int b, hg, a;
+  if (!decode_tile(p, c, wave_id(), b, hg, a)) return;
+  const int lane = threadIdx.x & 63;
+  const int h = hg * (64 / LPR) + lane / LPR;
+  BwdPipe<T, LPR, NM, FAR> w;
+  w.li = lane % LPR;
+  auto base = [&](const View& vw) {
+    return reinterpret_cast<const T*>(vw.p) + (int64_t)b * vw.sb + (int64_t)h * vw.sh;
+  };
+  auto mbase = [&](const MutView& vw) {
+    return reinterpret_cast<T*>(vw.p) + (int64_t)b * vw.sb + (int64_t)h * vw.sh;
+  };
+  w.q = base(p.q);
+  w.k = base(p.k);
+  w.v = base(p.v);
+  w.go = base(p.dout);
+  w.dq = mbase(p.dq);
+  w.dk = mbase(p.dk);
+  w.dv = mbase(p.dv);
+  w.qst = p.q.st;
+  w.kst = p.k.st;
+  w.vst = p.v.st;
+  w.gst = p.dout.st;
+  w.dqst = p.dq.st;
+  w.dkst = p.dk.st;
+  w.dvst = p.dv.st;
+  w.lse = p.lse + (int64_t)b * p.T * p.H + h;
+  w.lst = p.H;
+  w.scale = p.scale;
+  w.F = c.F;
+  w.T_ = p.T;
+  w.Tm1 = p.T - 1;
+  w.a = a;
+  w.end = min(a + c.P, p.T);
+  // Walk u = a-2 .. end+1 (slot of u is (u - a + 2) & 3).
+  const int u0 = a - 2, last = w.end + 1;
+  w.template prefetch<0>(u0);
+  for (int u = u0; u <= last; u += 4) {
+    w.template prefetch<1>(u + 1);
+    w.template compute<0>(u);
+    w.template prefetch<2>(u + 2);
+    w.template compute<1>(u + 1);
+    w.template prefetch<3>(u + 3);
+    w.template compute<2>(u + 2);
+    w.template prefetch<0>(u + 4);
+    w.template compute<3>(u + 3);
+  }
 }
 
 // ================================================================= dispatch
@@ -586,6 +989,11 @@ WalkCfg make_cfg(const Params& p, int lpr, const Pattern& pat) {
   // 16 positions (halo overhead <= 2/16) and at most 256.
   int P = 256;
   while (P > 16 && lanes_rows * ((p.T + P - 1) / P) < 8192) P >>= 1;
+  // A far offset inside the tile would make a wave re-read rows it loaded F
+  // steps earlier, long evicted from L2.  With the tile shrunk to F the far
+  // rows belong to the neighbouring tile, which a neighbouring wave walks at
+  // the same time, so they are L2 hits.
+  if (pat.far >= 16 && pat.far < P && (pat.far & (pat.far - 1)) == 0) P = pat.far;
   c.P = P;
   c.F = pat.far;
   if (pat.far >= P && pat.far % P == 0) {
@@ -607,10 +1015,14 @@ hipError_t launch_pattern(const Params& p, const WalkCfg& c, const Pattern& pat,
   const dim3 grid((unsigned)c.nwg), block(kWalkBlock);
 #define SBDA_WALK_CASE(NMV, FARV)                                                            \
   if (pat.nm == NMV && (pat.far != 0) == FARV) {                                             \
-    if (FWD)                                                                                 \
-      hipLaunchKernelGGL((fwd_walk<T, LPR, NMV, FARV, PRO>), grid, block, 0, st, p, c);     \
+    if (FWD && PRO)                                                                          \
+      hipLaunchKernelGGL((fwd_walk<T, LPR, NMV, FARV, true>), grid, block, 0, st, p, c);    \
+    else if (FWD)                                                                            \
+      hipLaunchKernelGGL((fwd_pipe<T, LPR, NMV, FARV>), grid, block, 0, st, p, c);          \
+    else if (PRO)                                                                            \
+      hipLaunchKernelGGL((bwd_walk<T, LPR, NMV, FARV, true>), grid, block, 0, st, p, c);    \
     else                                                                                     \
-      hipLaunchKernelGGL((bwd_walk<T, LPR, NMV, FARV, PRO>), grid, block, 0, st, p, c);     \
+      hipLaunchKernelGGL((bwd_pipe<T, LPR, NMV, FARV>), grid, block, 0, st, p, c);          \
     return hipGetLastError();                                                                \
   }
   SBDA_WALK_CASE(3, false)

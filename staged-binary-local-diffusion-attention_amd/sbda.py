@@ -107,6 +107,19 @@ def _shape_args(q, k, offs):
 
 # -------------------------------------------------------- raw entry points
 
+def _lse_storage(b: int, h: int, t: int, device) -> torch.Tensor:
+    """Per-row log-normalisers, stored position-major ``[B, T, H]`` (each
+    position's heads are adjacent, as in q/k/v memory) and handed out as a
+    ``[B, H, T]`` view."""
+    return torch.empty((b, t, h), dtype=torch.float32, device=device).permute(0, 2, 1)
+
+
+def _lse_buffer(lse: torch.Tensor) -> torch.Tensor:
+    """The ``[B, T, H]`` contiguous buffer behind a ``[B, H, T]`` lse view."""
+    buf = lse.permute(0, 2, 1)
+    return buf if buf.is_contiguous() else buf.contiguous()
+
+
 def sbda_forward(q, k, v, offsets) -> tuple[torch.Tensor, torch.Tensor]:
     """Forward without autograd: ``(out [B,H,T,D], lse [B,H,T] fp32)``."""
     offs = host_offsets(offsets)
@@ -115,7 +128,7 @@ def sbda_forward(q, k, v, offsets) -> tuple[torch.Tensor, torch.Tensor]:
     q, k, v = (_kernel_view(x) for x in (q, k, v))
     out = torch.empty_like(q)
     b, h, t, _ = q.shape
-    lse = torch.empty((b, h, t), dtype=torch.float32, device=q.device)
+    lse = _lse_storage(b, h, t, q.device)
     with torch.cuda.device(q.device):
         _lib.check(lib.sbda_forward(
             _ptr(q), _lib.strides(q), _ptr(k), _lib.strides(k), _ptr(v), _lib.strides(v),
@@ -131,7 +144,9 @@ def sbda_backward(q, k, v, grad_out, lse, offsets):
     q, k, v, grad_out = (_kernel_view(x) for x in (q, k, v, grad_out))
     if grad_out.shape != q.shape or grad_out.dtype != q.dtype:
         raise ValueError("grad_out must match q's shape and dtype")
-    lse = lse.contiguous()
+    if lse.shape != q.shape[:3] or lse.dtype != torch.float32:
+        raise ValueError("lse must be the fp32 [B,H,T] log-normalisers of the forward")
+    lse = _lse_buffer(lse)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     with torch.cuda.device(q.device):
         _lib.check(lib.sbda_backward(
@@ -236,7 +251,7 @@ class _FusedSBDAPrologue(torch.autograd.Function):
         wq, wk = _weight32(q_weight, d, q.device), _weight32(k_weight, d, q.device)
         cos, sin = rope_tables(t, d, theta, q.device)
         out = torch.empty_like(q)
-        lse = torch.empty((b, h, t), dtype=torch.float32, device=q.device)
+        lse = _lse_storage(b, h, t, q.device)
         with torch.cuda.device(q.device):
             _lib.check(lib.sbda_forward_prologue(
                 _ptr(q), _lib.strides(q), _ptr(k), _lib.strides(k), _ptr(v), _lib.strides(v),

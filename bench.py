@@ -28,6 +28,7 @@ if str(ROOT) not in sys.path:
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "SBDA attn fwd+bwd positions/s and achieved HBM GB/s at T=1M, D=64, bf16"
+TRAFFIC_FILE = ROOT / "profiles" / "sbda_hbm_traffic.json"
 
 
 def sbda_offsets(layer: int) -> tuple[int, ...]:
@@ -106,7 +107,13 @@ def main() -> int:
     ap.add_argument("--head-dim", type=int, default=64)
     ap.add_argument("--layers", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="for rocprofv3 counter runs: one untimed-warmup-free step, no CPU "
+                         "baseline, preceded by a 256 MiB device copy whose counter readings "
+                         "calibrate FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
+    if args.profile_pass:
+        args.steps, args.warmup, args.no_cpu_baseline = 1, 0, True
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -127,6 +134,28 @@ def main() -> int:
                    .to(dtype).permute(0, 2, 1, 3) for _ in range(4))
     offsets = [sbda_offsets(l) for l in range(1, layers + 1)]
     stream = torch.cuda.current_stream(dev)
+    if args.profile_pass:
+        src = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    # Measured copy peak (1 GiB device-to-device copy), for the second
+    # roofline fraction.
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    cps = []
+    for _ in range(5):
+        c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        c0.record(stream)
+        dst.copy_(src)
+        c1.record(stream)
+        torch.cuda.synchronize()
+        cps.append(c0.elapsed_time(c1))
+    copy_gbs = 2 * (1 << 30) / (sorted(cps)[2] * 1e-3) / 1e9
+    del src, dst
 
     fwd_ev, bwd_ev = [], []
 
@@ -167,6 +196,14 @@ def main() -> int:
     bwd_gbs = bwd_b / (bwd_ms * 1e-3) / 1e9
     fwd_gbs = fwd_b / (fwd_ms * 1e-3) / 1e9
     dominant = "backward" if bwd_ms >= fwd_ms else "forward"
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        try:
+            rec = json.loads(TRAFFIC_FILE.read_text())
+            if rec.get("length") == t and rec.get("heads") == h and rec.get("head_dim") == d:
+                traffic = rec[f"{dominant}_bytes_per_launch"]
+        except (ValueError, KeyError):
+            traffic = None
 
     result = {
         "metric": METRIC,
@@ -186,6 +223,8 @@ def main() -> int:
                    "layout": "[B,T,H,D] memory as [B,H,T,D] views"},
         "achieved_gbs": gbs,
         "hbm_fraction": gbs / HBM_PEAK_GBS,
+        "copy_peak_gbs": copy_gbs,
+        "copy_fraction": gbs / copy_gbs,
         "forward_ms_per_layer": fwd_ms,
         "backward_ms_per_layer": bwd_ms,
         "forward_gbs": fwd_gbs,
@@ -197,7 +236,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": (bwd_gbs if dominant == "backward" else fwd_gbs) / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": traffic,
             "algorithmic_bytes_per_launch": bwd_b if dominant == "backward" else fwd_b,
         },
         "cpu_baseline": None,

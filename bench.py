@@ -96,6 +96,62 @@ def cpu_baseline(layers: int, h: int, d: int, seconds_target: float = 15.0) -> d
     }
 
 
+def _median_ms(torch, fn, reps: int = 5) -> float:
+    fn()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b))
+    return sorted(ts)[reps // 2]
+
+
+def other_configs(torch, sbda, dev) -> dict:
+    """The BASELINE configs other than the metric's, measured after the timed
+    region (medians of 5 runs each)."""
+    res = {}
+    gen = torch.Generator(device=dev).manual_seed(99)
+
+    def rnd(b, t, h, d):
+        return (torch.randn(b, t, h, d, generator=gen, device=dev)
+                .to(torch.bfloat16).permute(0, 2, 1, 3))
+
+    # Config 2: one forward layer, B=8, T=4096, H=8, D=64, layers 1..12.  The
+    # 128 MiB of q/k/v/o fit in the 256 MB Infinity Cache, so these numbers
+    # are cache-resident, not HBM rates.
+    q, k, v = rnd(8, 4096, 8, 64), rnd(8, 4096, 8, 64), rnd(8, 4096, 8, 64)
+    per = []
+    for layer in range(1, 13):
+        offs = sbda_offsets(layer)
+        per.append(_median_ms(torch, lambda: sbda.sbda_forward(q, k, v, offs)) * 1e3)
+    res["config2_forward_us_per_layer"] = {"layers_1_to_12": per, "cache_resident": True}
+    del q, k, v
+    # Config 3: 15-layer fwd+bwd, B=4, T=32768, H=8, D=64, q/k head-RMSNorm +
+    # RoPE(10000) fused into the kernels (weights 1), through autograd.
+    b, t = 4, 32768
+    q, k, v, go = (rnd(b, t, 8, 64).detach().requires_grad_() for _ in range(4))
+    wq = torch.ones(64, device=dev, requires_grad=True)
+    wk = torch.ones(64, device=dev, requires_grad=True)
+    offs_t = [torch.tensor(sbda_offsets(l), dtype=torch.int32, device=dev) for l in range(1, 16)]
+
+    def cfg3():
+        for off in offs_t:
+            out = sbda.fused_sbda_prologue(q, k, v, off, wq, wk, theta=10000.0)
+            torch.autograd.grad(out, (q, k, v, wq, wk), go.detach())
+
+    ms = _median_ms(torch, cfg3)
+    fwd_b, bwd_b = algorithmic_bytes(b * t * 8, 64, 2)
+    res["config3_prologue_fwd_bwd"] = {
+        "ms_per_step": ms, "positions_per_s": b * t / (ms * 1e-3),
+        "algorithmic_gbs": (fwd_b + bwd_b) * 15 / (ms * 1e-3) / 1e9,
+        "note": "B=4 T=32768 H=8 D=64 bf16, 15 layers, norm+RoPE fused, via autograd"}
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -241,8 +297,15 @@ def main() -> int:
         },
         "cpu_baseline": None,
     }
+    result["config4_forward_only"] = {
+        "ms_per_20_layers": fwd_ms * layers,
+        "algorithmic_gbs": fwd_b / (fwd_ms * 1e-3) / 1e9,
+        "note": "sum of the timed forward launches above (same T=2^20 inputs)"}
     del q, k, v, go
     torch.cuda.empty_cache()
+    if not args.profile_pass:
+        result.update(other_configs(torch, sbda, dev))
+        torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(layers, h, d)
     print(json.dumps(result), flush=True)

@@ -304,3 +304,64 @@ def test_tile_edges_and_offset_patterns(t, offs):
     _close(_fused(q, k, v, offs, g), _oracle(q, k, v, offs, g), LOW_TOL, f"T={t} {offs}")
     q, k, v, g = _inputs(1, t, 8, 64, torch.float32, seed=t * 37 + sum(offs))
     _close(_fused(q, k, v, offs, g), _oracle(q, k, v, offs, g), FP32_TOL, f"fp32 T={t} {offs}")
+
+
+# ------------------------------------------------------------ module level
+
+def _oracle_module_forward(m, x, valid_mask=None):
+    """The reference module's fused-route forward (left_v2.py:234-306),
+    restated with the oracle's prologue and gather attention."""
+    b, t, dim = x.shape
+    q = (x @ m.q.weight.T).view(b, t, m.heads, m.head_dim)
+    k = (x @ m.k.weight.T).view(b, t, m.kv_heads, m.head_dim)
+    v = (x @ m.v.weight.T).view(b, t, m.kv_heads, m.head_dim)
+    q, k = ref.prologue(q, k, m.q_norm.weight, m.k_norm.weight, m.rope_theta)
+    att = ref.gather_attention(q.permute(0, 2, 1, 3), k.permute(0, 2, 1, 3),
+                               v.permute(0, 2, 1, 3), m.offsets)
+    out = att.transpose(1, 2).reshape(b, t, dim) @ m.out.weight.T
+    if valid_mask is not None:
+        out = out * valid_mask[:, :, None].to(out.dtype)
+    return out
+
+
+@pytest.mark.parametrize("layer,kv_heads", [(1, None), (3, None), (9, None), (4, 4)])
+def test_sbdattention_module_matches_oracle_module(layer, kv_heads):
+    torch.manual_seed(50 + layer)
+    dim, heads, t = 512, 8, 700
+    m = sbda_amd.SBDAttention(dim, heads, layer, kv_heads=kv_heads, rope_theta=10000.0,
+                              total_layers=12)
+    with torch.no_grad():
+        m.q_norm.weight.mul_(1 + 0.1 * torch.randn(m.head_dim))
+        m.k_norm.weight.mul_(1 + 0.1 * torch.randn(m.head_dim))
+    x = torch.randn(2, t, dim)
+    valid = torch.ones(2, t, dtype=torch.bool)
+    valid[1, 650:] = False                         # right padding: fused-eligible
+    g = torch.randn(2, t, dim)
+    md = m.to(DEV)
+    xd = x.to(DEV).requires_grad_()
+    out = md(xd, valid.to(DEV))
+    out.backward(g.to(DEV))
+    torch.cuda.synchronize()
+    mc = sbda_amd.SBDAttention(dim, heads, layer, kv_heads=kv_heads, rope_theta=10000.0,
+                               total_layers=12)
+    mc.load_state_dict({k_: v_.cpu() for k_, v_ in md.state_dict().items()})
+    xc = x.clone().requires_grad_()
+    want = _oracle_module_forward(mc, xc, valid)
+    want.backward(g)
+    tol = dict(rtol=1e-4, atol=1e-4)
+    torch.testing.assert_close(out.detach().cpu(), want.detach(), **tol)
+    torch.testing.assert_close(xd.grad.cpu(), xc.grad, **tol)
+    for (name, p), (_, pc) in zip(md.named_parameters(), mc.named_parameters()):
+        scale = pc.grad.abs().max().item() + 1e-6
+        err = (p.grad.cpu() - pc.grad).abs().max().item()
+        assert err / scale < 1e-4, f"{name}: {err} vs scale {scale}"
+
+
+def test_sbdattention_module_rejects_eager_only_inputs():
+    m = sbda_amd.SBDAttention(64, 4, 3).to(DEV)
+    x = torch.randn(1, 8, 64, device=DEV)
+    holes = torch.tensor([[True, False, True, True, True, True, True, True]], device=DEV)
+    with pytest.raises(NotImplementedError, match="interior holes"):
+        m(x, holes)
+    with pytest.raises(NotImplementedError, match="seam_reset"):
+        m(x, None, torch.zeros(1, 8, dtype=torch.bool, device=DEV))

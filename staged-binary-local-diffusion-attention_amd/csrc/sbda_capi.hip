@@ -17,7 +17,8 @@ void direct_partials(const Params& p, int esz, int64_t* parts_q, int64_t* parts_
 bool walk_applies(const Params& p, int dtype);
 hipError_t walk_forward(const Params& p, int dtype, bool pro, hipStream_t st);
 hipError_t walk_backward(const Params& p, int dtype, bool pro, hipStream_t st);
-void walk_partials(const Params& p, int dtype, int64_t* parts_q, int64_t* parts_k);
+void walk_partials(const Params& p, int dtype, int64_t* parts_q, int64_t* parts_k,
+                   int64_t* tab_floats);
 
 namespace {
 
@@ -138,9 +139,12 @@ int forward_impl(bool pro, const void* q, const int64_t* qs, const void* k, cons
   return hip_status(e, "sbda forward launch");
 }
 
-void partials(const Params& p, int dtype, int64_t* pq, int64_t* pk) {
+// Workspace of the prologue backward: weight-gradient partial rows for the
+// query and key sides, then (walk kernels) the per-(row, slot) weight table.
+void partials(const Params& p, int dtype, int64_t* pq, int64_t* pk, int64_t* tab) {
+  *tab = 0;
   if (walk_applies(p, dtype))
-    walk_partials(p, dtype, pq, pk);
+    walk_partials(p, dtype, pq, pk, tab);
   else
     direct_partials(p, esize(dtype), pq, pk);
 }
@@ -172,8 +176,9 @@ int backward_impl(bool pro, const void* q, const int64_t* qs, const void* k, con
   if (pro) {
     if (!wq || !wk || !rc || !rs || !dwq || !dwk)
       return fail(SBDA_ERR_VALUE, "prologue: null weight, weight-gradient or RoPE table");
-    partials(p, dtype, &pq, &pk);
-    const int64_t need = (pq + pk) * p.D * (int64_t)sizeof(float);
+    int64_t tab = 0;
+    partials(p, dtype, &pq, &pk, &tab);
+    const int64_t need = ((pq + pk) * p.D + tab) * (int64_t)sizeof(float);
     if (ws == nullptr || ws_bytes < need)
       return fail(SBDA_ERR_VALUE, "prologue backward: workspace of %lld bytes needed, %lld given",
                   (long long)need, (long long)ws_bytes);
@@ -185,6 +190,7 @@ int backward_impl(bool pro, const void* q, const int64_t* qs, const void* k, con
     p.eps = eps;
     p.dwq_part = reinterpret_cast<float*>(ws);
     p.dwk_part = p.dwq_part + pq * p.D;
+    p.tab = p.dwk_part + pk * p.D;
   }
   hipError_t e = walk_applies(p, dtype) ? walk_backward(p, dtype, pro, st)
                                         : direct_backward(p, dtype, pro, st);
@@ -241,9 +247,9 @@ int64_t sbda_backward_prologue_workspace(int64_t batch, int64_t heads, int64_t k
   Params p;
   int rc = check_problem(batch, heads, kv_heads, length, head_dim, dtype, offsets, n, p);
   if (rc) return -rc;
-  int64_t pq = 0, pk = 0;
-  partials(p, dtype, &pq, &pk);
-  return (pq + pk) * p.D * (int64_t)sizeof(float);
+  int64_t pq = 0, pk = 0, tab = 0;
+  partials(p, dtype, &pq, &pk, &tab);
+  return ((pq + pk) * p.D + tab) * (int64_t)sizeof(float);
 }
 
 int sbda_backward_prologue(const void* q, const int64_t* qs, const void* k, const int64_t* ks,

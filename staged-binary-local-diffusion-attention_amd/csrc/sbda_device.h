@@ -244,6 +244,65 @@ struct Prologue {
     return r;
   }
 
+  // The lane's norm weights in register-slot order (split layout).
+  __device__ static inline void load_w(const float* __restrict__ w, int li, int D,
+                                       float (&wl)[VEC]) {
+    const int half = D >> 1;
+    const bool on = li * HV < half;
+#pragma unroll
+    for (int i = 0; i < HV; ++i) {
+      wl[i] = on ? w[li * HV + i] : 0.f;
+      wl[HV + i] = on ? w[half + li * HV + i] : 0.f;
+    }
+  }
+
+  // rsqrt(mean(x^2) + eps) of a raw row.
+  __device__ static inline float rms_factor(const float (&x)[VEC], int D, float eps) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) ss = __builtin_fmaf(x[i], x[i], ss);
+    ss = row_sum<LPR>(ss);
+    return __builtin_amdgcn_rsqf(__fadd_rn(__fdiv_rn(ss, (float)D), eps));
+  }
+
+  // forward() with the weights already in registers.
+  __device__ static inline float forward_w(float (&x)[VEC], const float (&wl)[VEC],
+                                           const float (&c)[HV], const float (&s)[HV], int D,
+                                           float eps) {
+    const float r = rms_factor(x, D, eps);
+#pragma unroll
+    for (int i = 0; i < HV; ++i) {
+      const float y1 = __fmul_rn(__fmul_rn(x[i], r), wl[i]);
+      const float y2 = __fmul_rn(__fmul_rn(x[HV + i], r), wl[HV + i]);
+      x[i] = __fadd_rn(__fmul_rn(y1, c[i]), -__fmul_rn(y2, s[i]));
+      x[HV + i] = __fadd_rn(__fmul_rn(y2, c[i]), __fmul_rn(y1, s[i]));
+    }
+    return r;
+  }
+
+  // backward() with the weights already in registers.
+  __device__ static inline void backward_w(float (&g)[VEC], const float (&x)[VEC], float r,
+                                           const float (&wl)[VEC], const float (&c)[HV],
+                                           const float (&s)[HV], int D, float (&dw)[VEC]) {
+    float dn[VEC], n[VEC];
+    float nd = 0.f;
+#pragma unroll
+    for (int i = 0; i < HV; ++i) {
+      const float dy1 = g[i] * c[i] + g[HV + i] * s[i];
+      const float dy2 = g[HV + i] * c[i] - g[i] * s[i];
+      n[i] = x[i] * r;
+      n[HV + i] = x[HV + i] * r;
+      dw[i] += dy1 * n[i];
+      dw[HV + i] += dy2 * n[HV + i];
+      dn[i] = dy1 * wl[i];
+      dn[HV + i] = dy2 * wl[HV + i];
+      nd += n[i] * dn[i] + n[HV + i] * dn[HV + i];
+    }
+    nd = row_sum<LPR>(nd) / (float)D;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) g[i] = r * (dn[i] - n[i] * nd);
+  }
+
   // g: gradient w.r.t. the roped row (fp32), x: raw row, r: rsqrt factor.
   // Writes the gradient w.r.t. the raw row into g and adds this row's
   // contribution to the weight gradient into dw (same register slots).

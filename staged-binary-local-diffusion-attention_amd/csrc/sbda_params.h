@@ -34,6 +34,7 @@ struct Params {
   float eps;
   float* dwq_part;             // [parts, D] fp32 per-block partial sums
   float* dwk_part;
+  float* tab;                  // prologue backward: per (row, slot) (p, scale * dS), fp32
 };
 
 enum DType : int { kBF16 = 0, kFP16 = 1, kFP32 = 2 };

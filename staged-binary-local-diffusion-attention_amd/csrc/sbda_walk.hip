@@ -943,6 +943,497 @@ __global__ __launch_bounds__(kWalkBlock) void bwd_pipe(Params p, WalkCfg c) {
   }
 }
 
+// ============================================== pipelined walks, fused prologue
+//
+// The prologue (head-RMSNorm + RoPE of q and k) is applied to each raw row
+// once, when it arrives; roped rows are kept in fp32.  Rows are in the split
+// layout (a lane holds the same positions of both halves, so RoPE partners
+// share a lane); v and dO stay raw and their dot products use v_dot2.
+//
+// The backward runs as two walks so that each fits in registers:
+//   A (query side): per query u, p_s and dS_s, dQ (through the transposed
+//     prologue) and, per (row, slot), the pair (p_s, scale * dS_s) into a
+//     workspace table [B, T, H, 2 * NS] (fp32);
+//   B (key side): per key j, dK/dV from queries j + n (near slots) and j + F
+//     (far slot) using that table -- no weight recomputation -- then dK
+//     through the transposed prologue.
+
+template <typename T>
+__device__ inline Raw load_raw_split(const T* __restrict__ row, int li, int D) {
+  constexpr int HV = VecOf<T>::value / 2;
+  const uint2 x = *reinterpret_cast<const uint2*>(row + li * HV);
+  const uint2 y = *reinterpret_cast<const uint2*>(row + (D >> 1) + li * HV);
+  return Raw{{x.x, x.y, y.x, y.y}};
+}
+
+template <typename T, int LPR>
+struct ProBase {
+  static constexpr int VEC = VecOf<T>::value;
+  static constexpr int HV = VEC / 2;
+  using PL = Prologue<T, LPR>;
+  const float* __restrict__ rc;
+  const float* __restrict__ rs;
+  float eps;
+  int li, D, Tm1;
+  float wq[VEC], wk[VEC];
+
+  __device__ inline void init(const Params& p, int lane_in_row) {
+    li = lane_in_row;
+    D = p.D;
+    Tm1 = p.T - 1;
+    rc = p.rope_cos;
+    rs = p.rope_sin;
+    eps = p.eps;
+    PL::load_w(p.wq, li, D, wq);
+    PL::load_w(p.wk, li, D, wk);
+  }
+  __device__ inline void cs(int t, float (&c)[HV], float (&s)[HV]) const {
+    PL::load_cs(rc, rs, t, li, D, c, s);
+  }
+  // Widens a raw q/k row and applies the prologue; returns the rms factor.
+  __device__ inline float rope(const Raw& r, const float (&w)[VEC], const float (&c)[HV],
+                               const float (&s)[HV], float (&x)[VEC]) const {
+    widen<T>(r, x);
+    return PL::forward_w(x, w, c, s, D, eps);
+  }
+};
+
+template <typename T, int LPR, int NM, bool FAR>
+struct FwdPipePro : ProBase<T, LPR> {
+  using B_ = ProBase<T, LPR>;
+  using B_::VEC;
+  using B_::HV;
+  static constexpr int NN = NearSet<NM>::count;
+  static constexpr int NS = NN + (FAR ? 1 : 0);
+
+  const T* __restrict__ q;
+  const T* __restrict__ k;
+  const T* __restrict__ v;
+  T* __restrict__ o;
+  float* __restrict__ lse;
+  int64_t qst, kst, vst, ost;
+  int lst, F;
+  float scale;
+  Raw kraw[2], qraw[2], vraw[2], klr[2], vlr[2];
+  float cc[2][HV], ss[2][HV], clc[2][HV], cls[2][HV];
+  float kq[4][VEC], vr[4][VEC];
+
+  template <int R>
+  __device__ inline void prefetch(int t) {
+    const int tc = clampi(t, this->Tm1);
+    kraw[R & 1] = load_raw_split<T>(k + (int64_t)tc * kst, this->li, this->D);
+    qraw[R & 1] = load_raw_split<T>(q + (int64_t)tc * qst, this->li, this->D);
+    vraw[R & 1] = load_raw_split<T>(v + (int64_t)tc * vst, this->li, this->D);
+    this->cs(tc, cc[R & 1], ss[R & 1]);
+    if constexpr (FAR) {
+      const int tf = clampi(t - F, this->Tm1);
+      klr[R & 1] = load_raw_split<T>(k + (int64_t)tf * kst, this->li, this->D);
+      vlr[R & 1] = load_raw_split<T>(v + (int64_t)tf * vst, this->li, this->D);
+      this->cs(tf, clc[R & 1], cls[R & 1]);
+    }
+  }
+
+  template <int R>
+  __device__ inline void compute(int t, bool store) {
+    this->rope(kraw[R & 1], this->wk, cc[R & 1], ss[R & 1], kq[R]);
+    widen<T>(vraw[R & 1], vr[R]);
+    float qr[VEC];
+    this->rope(qraw[R & 1], this->wq, cc[R & 1], ss[R & 1], qr);
+    float sc[NS];
+    bool ok[NS];
+    int idx = 0;
+#pragma unroll
+    for (int n = 0; n < 3; ++n) {
+      if (NM & (1 << n)) {
+        ok[idx] = t - n >= 0;
+        sc[idx] = row_sum<LPR>(dot_partial<VEC>(qr, kq[(R + 4 - n) & 3])) * scale;
+        ++idx;
+      }
+    }
+    float vf[VEC];
+    if constexpr (FAR) {
+      float kf[VEC];
+      this->rope(klr[R & 1], this->wk, clc[R & 1], cls[R & 1], kf);
+      widen<T>(vlr[R & 1], vf);
+      ok[NS - 1] = t - F >= 0;
+      sc[NS - 1] = row_sum<LPR>(dot_partial<VEC>(qr, kf)) * scale;
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) m = ok[s] ? fmaxf(m, sc[s]) : m;
+    float w[NS], l = 0.f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      w[s] = ok[s] ? fast_exp(sc[s] - m) : 0.f;
+      l += w[s];
+    }
+    float acc[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+    idx = 0;
+#pragma unroll
+    for (int n = 0; n < 3; ++n) {
+      if (NM & (1 << n)) {
+        const int slot = (R + 4 - n) & 3;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] = __builtin_fmaf(w[idx], vr[slot][e], acc[e]);
+        ++idx;
+      }
+    }
+    if constexpr (FAR) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[e] = __builtin_fmaf(w[NS - 1], vf[e], acc[e]);
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] *= inv;
+    if (store) {
+      store_row<T, true>(o + (int64_t)t * ost, this->li, this->D, acc);
+      if (this->li == 0) lse[(int64_t)t * lst] = l > 0.f ? m + fast_log(l) : INFINITY;
+    }
+  }
+};
+
+template <typename T, int LPR, int NM, bool FAR>
+__global__ __launch_bounds__(kWalkBlock) void fwd_pipe_pro(Params p, WalkCfg c) {
+  int b, hg, a;
+  if (!decode_tile(p, c, wave_id(), b, hg, a)) return;
+  const int lane = threadIdx.x & 63;
+  const int h = hg * (64 / LPR) + lane / LPR;
+  FwdPipePro<T, LPR, NM, FAR> w;
+  w.init(p, lane % LPR);
+  w.q = reinterpret_cast<const T*>(p.q.p) + (int64_t)b * p.q.sb + (int64_t)h * p.q.sh;
+  w.k = reinterpret_cast<const T*>(p.k.p) + (int64_t)b * p.k.sb + (int64_t)h * p.k.sh;
+  w.v = reinterpret_cast<const T*>(p.v.p) + (int64_t)b * p.v.sb + (int64_t)h * p.v.sh;
+  w.o = reinterpret_cast<T*>(p.o.p) + (int64_t)b * p.o.sb + (int64_t)h * p.o.sh;
+  w.qst = p.q.st;
+  w.kst = p.k.st;
+  w.vst = p.v.st;
+  w.ost = p.o.st;
+  w.lse = p.lse + (int64_t)b * p.T * p.H + h;
+  w.lst = p.H;
+  w.scale = p.scale;
+  w.F = c.F;
+  const int end = min(a + c.P, p.T);
+  const int t0 = a - 2;   // slot of t is (t - a + 2) & 3
+  w.template prefetch<0>(t0);
+  for (int t = t0; t < end; t += 4) {
+    w.template prefetch<1>(t + 1);
+    w.template compute<0>(t, t >= a && t < end);
+    w.template prefetch<2>(t + 2);
+    w.template compute<1>(t + 1, t + 1 >= a && t + 1 < end);
+    w.template prefetch<3>(t + 3);
+    w.template compute<2>(t + 2, t + 2 >= a && t + 2 < end);
+    w.template prefetch<0>(t + 4);
+    w.template compute<3>(t + 3, t + 3 >= a && t + 3 < end);
+  }
+}
+
+// ---- backward A: query side
+
+template <typename T, int LPR, int NM, bool FAR>
+struct BwdQPro : ProBase<T, LPR> {
+  using B_ = ProBase<T, LPR>;
+  using B_::VEC;
+  using B_::HV;
+  using PL = typename B_::PL;
+  static constexpr int NN = NearSet<NM>::count;
+  static constexpr int NS = NN + (FAR ? 1 : 0);
+
+  const T* __restrict__ q;
+  const T* __restrict__ k;
+  const T* __restrict__ v;
+  const T* __restrict__ go;
+  T* __restrict__ dq;
+  const float* __restrict__ lse;
+  float* __restrict__ tab;   // (p, scale * dS) per (row, slot)
+  int64_t qst, kst, vst, gst, dqst, tst;
+  int lst, F, a, end;
+  float scale;
+  Raw kraw[2], qraw[2], graw[2], klr[2], vlr[2];
+  float lv[2];
+  float cc[2][HV], ss[2][HV], clc[2][HV], cls[2][HV];
+  float kq[4][VEC];
+  Raw vr[4];
+  float dw[VEC];
+
+  template <int R>
+  __device__ inline void prefetch(int u) {
+    const int uc = clampi(u, this->Tm1);
+    kraw[R & 1] = load_raw_split<T>(k + (int64_t)uc * kst, this->li, this->D);
+    vr[R] = load_raw_split<T>(v + (int64_t)uc * vst, this->li, this->D);
+    qraw[R & 1] = load_raw_split<T>(q + (int64_t)uc * qst, this->li, this->D);
+    graw[R & 1] = load_raw_split<T>(go + (int64_t)uc * gst, this->li, this->D);
+    lv[R & 1] = lse[(int64_t)uc * lst];
+    this->cs(uc, cc[R & 1], ss[R & 1]);
+    if constexpr (FAR) {
+      const int ul = clampi(u - F, this->Tm1);
+      klr[R & 1] = load_raw_split<T>(k + (int64_t)ul * kst, this->li, this->D);
+      vlr[R & 1] = load_raw_split<T>(v + (int64_t)ul * vst, this->li, this->D);
+      this->cs(ul, clc[R & 1], cls[R & 1]);
+    }
+  }
+
+  template <int R>
+  __device__ inline void compute(int u) {
+    this->rope(kraw[R & 1], this->wk, cc[R & 1], ss[R & 1], kq[R]);
+    float qx[VEC], qr[VEC];
+    widen<T>(qraw[R & 1], qx);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) qr[e] = qx[e];
+    const float rq = PL::forward_w(qr, this->wq, cc[R & 1], ss[R & 1], this->D, this->eps);
+    float kf[VEC];
+    if constexpr (FAR) this->rope(klr[R & 1], this->wk, clc[R & 1], cls[R & 1], kf);
+    const float* ks[NS];
+    const Raw* vs[NS];
+    bool ok[NS];
+    int idx = 0;
+#pragma unroll
+    for (int n = 0; n < 3; ++n) {
+      if (NM & (1 << n)) {
+        ks[idx] = kq[(R + 4 - n) & 3];
+        vs[idx] = &vr[(R + 4 - n) & 3];
+        ok[idx] = u - n >= 0;
+        ++idx;
+      }
+    }
+    if constexpr (FAR) {
+      ks[NS - 1] = kf;
+      vs[NS - 1] = &vlr[R & 1];
+      ok[NS - 1] = u - F >= 0;
+    }
+    float pp[NS], dp[NS], delta = 0.f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      float a_ = 0.f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) a_ = __builtin_fmaf(qr[e], ks[s][e], a_);
+      const float sc = row_sum<LPR>(a_) * scale;
+      dp[s] = row_sum<LPR>(dot_raw<T>(graw[R & 1], *vs[s]));
+      pp[s] = ok[s] ? fast_exp(sc - lv[R & 1]) : 0.f;
+      delta = __builtin_fmaf(pp[s], dp[s], delta);
+    }
+    if (u >= a && u < end) {
+      float g[VEC], ds[NS];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) g[e] = 0.f;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        ds[s] = pp[s] * (dp[s] - delta) * scale;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) g[e] = __builtin_fmaf(ds[s], ks[s][e], g[e]);
+      }
+      PL::backward_w(g, qx, rq, this->wq, cc[R & 1], ss[R & 1], this->D, dw);
+      store_row<T, true>(dq + (int64_t)u * dqst, this->li, this->D, g);
+      float* trow = tab + (int64_t)u * tst;
+#pragma unroll
+      for (int vix = 0; vix < 2 * NS; ++vix) {
+        const int s = vix >> 1;
+        if (vix % LPR == this->li) trow[vix] = (vix & 1) ? ds[s] : pp[s];
+      }
+    }
+  }
+};
+
+// ---- backward B: key side
+
+template <typename T, int LPR, int NM, bool FAR>
+struct BwdKPro : ProBase<T, LPR> {
+  using B_ = ProBase<T, LPR>;
+  using B_::VEC;
+  using B_::HV;
+  using PL = typename B_::PL;
+  static constexpr int NN = NearSet<NM>::count;
+  static constexpr int NS = NN + (FAR ? 1 : 0);
+
+  const T* __restrict__ q;
+  const T* __restrict__ k;
+  const T* __restrict__ go;
+  T* __restrict__ dk;
+  T* __restrict__ dv;
+  const float* __restrict__ tab;
+  int64_t qst, kst, gst, dkst, dvst, tst;
+  int F, a, end, T_;
+  Raw qraw[2], kraw[2], qir[2], gir[2];
+  Raw gr[4];
+  float cc[2][HV], ss[2][HV], cic[2][HV], cis[2][HV], ckc[2][HV], cks[2][HV];
+  float tp[2][NS], td[2][NS];   // (p, scale dS) feeding key u - 2, per slot
+  float qq[4][VEC];
+  float dw[VEC];
+
+  template <int R>
+  __device__ inline void prefetch(int u) {
+    const int uc = clampi(u, this->Tm1);
+    qraw[R & 1] = load_raw_split<T>(q + (int64_t)uc * qst, this->li, this->D);
+    gr[R] = load_raw_split<T>(go + (int64_t)uc * gst, this->li, this->D);
+    this->cs(uc, cc[R & 1], ss[R & 1]);
+    const int j = u - 2;
+    const int jc = clampi(j, this->Tm1);
+    kraw[R & 1] = load_raw_split<T>(k + (int64_t)jc * kst, this->li, this->D);
+    this->cs(jc, ckc[R & 1], cks[R & 1]);
+    int idx = 0;
+#pragma unroll
+    for (int n = 0; n < 3; ++n) {
+      if (NM & (1 << n)) {
+        const float* trow = tab + (int64_t)clampi(j + n, this->Tm1) * tst;
+        tp[R & 1][idx] = trow[2 * idx];
+        td[R & 1][idx] = trow[2 * idx + 1];
+        ++idx;
+      }
+    }
+    if constexpr (FAR) {
+      const int ic = clampi(j + F, this->Tm1);
+      const float* trow = tab + (int64_t)ic * tst;
+      tp[R & 1][NS - 1] = trow[2 * (NS - 1)];
+      td[R & 1][NS - 1] = trow[2 * (NS - 1) + 1];
+      qir[R & 1] = load_raw_split<T>(q + (int64_t)ic * qst, this->li, this->D);
+      gir[R & 1] = load_raw_split<T>(go + (int64_t)ic * gst, this->li, this->D);
+      this->cs(ic, cic[R & 1], cis[R & 1]);
+    }
+  }
+
+  template <int R>
+  __device__ inline void compute(int u) {
+    this->rope(qraw[R & 1], this->wq, cc[R & 1], ss[R & 1], qq[R]);
+    const int j = u - 2;
+    if (j >= a && j < end) {
+      float ak[VEC], av[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) { ak[e] = 0.f; av[e] = 0.f; }
+      int idx = 0;
+#pragma unroll
+      for (int n = 0; n < 3; ++n) {
+        if (NM & (1 << n)) {
+          const int slot = (R + 2 + n) & 3;   // query j + n
+          const bool there = j + n < T_;
+          const float cs_ = there ? td[R & 1][idx] : 0.f;
+          const float cp_ = there ? tp[R & 1][idx] : 0.f;
+          float gx[VEC];
+          widen<T>(gr[slot], gx);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            ak[e] = __builtin_fmaf(cs_, qq[slot][e], ak[e]);
+            av[e] = __builtin_fmaf(cp_, gx[e], av[e]);
+          }
+          ++idx;
+        }
+      }
+      if constexpr (FAR) {
+        const bool there = j + F < T_;
+        const float cs_ = there ? td[R & 1][NS - 1] : 0.f;
+        const float cp_ = there ? tp[R & 1][NS - 1] : 0.f;
+        float qf[VEC], gx[VEC];
+        this->rope(qir[R & 1], this->wq, cic[R & 1], cis[R & 1], qf);
+        widen<T>(gir[R & 1], gx);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          ak[e] = __builtin_fmaf(cs_, qf[e], ak[e]);
+          av[e] = __builtin_fmaf(cp_, gx[e], av[e]);
+        }
+      }
+      float kx[VEC];
+      widen<T>(kraw[R & 1], kx);
+      const float rk = PL::rms_factor(kx, this->D, this->eps);
+      PL::backward_w(ak, kx, rk, this->wk, ckc[R & 1], cks[R & 1], this->D, dw);
+      store_row<T, true>(dk + (int64_t)j * dkst, this->li, this->D, ak);
+      store_row<T, true>(dv + (int64_t)j * dvst, this->li, this->D, av);
+    }
+  }
+};
+
+template <typename W>
+__device__ inline void walk4(W& w, int first, int last) {
+  w.template prefetch<0>(first);
+  for (int u = first; u <= last; u += 4) {
+    w.template prefetch<1>(u + 1);
+    w.template compute<0>(u);
+    w.template prefetch<2>(u + 2);
+    w.template compute<1>(u + 1);
+    w.template prefetch<3>(u + 3);
+    w.template compute<2>(u + 2);
+    w.template prefetch<0>(u + 4);
+    w.template compute<3>(u + 3);
+  }
+}
+
+template <typename T, int LPR, int NM, bool FAR>
+__global__ __launch_bounds__(kWalkBlock) void bwd_q_pro(Params p, WalkCfg c) {
+  constexpr int VEC = VecOf<T>::value;
+  const int64_t wave = wave_id();
+  int b, hg, a;
+  const bool live = decode_tile(p, c, wave, b, hg, a);
+  const int lane = threadIdx.x & 63;
+  BwdQPro<T, LPR, NM, FAR> w;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) w.dw[e] = 0.f;
+  if (live) {
+    const int h = hg * (64 / LPR) + lane / LPR;
+    w.init(p, lane % LPR);
+    auto base = [&](const View& vw) {
+      return reinterpret_cast<const T*>(vw.p) + (int64_t)b * vw.sb + (int64_t)h * vw.sh;
+    };
+    w.q = base(p.q);
+    w.k = base(p.k);
+    w.v = base(p.v);
+    w.go = base(p.dout);
+    w.dq = reinterpret_cast<T*>(p.dq.p) + (int64_t)b * p.dq.sb + (int64_t)h * p.dq.sh;
+    w.qst = p.q.st;
+    w.kst = p.k.st;
+    w.vst = p.v.st;
+    w.gst = p.dout.st;
+    w.dqst = p.dq.st;
+    w.lse = p.lse + (int64_t)b * p.T * p.H + h;
+    w.lst = p.H;
+    w.tab = p.tab + ((int64_t)b * p.T * p.H + h) * (2 * w.NS);
+    w.tst = (int64_t)p.H * 2 * w.NS;
+    w.scale = p.scale;
+    w.F = c.F;
+    w.a = a;
+    w.end = min(a + c.P, p.T);
+    // Queries a-2, a-1 only fill the near-source rotation (slot of u is (u - a + 2) & 3).
+    walk4(w, a - 2, w.end - 1);
+  }
+  write_wave_partial<T, LPR, true>(w.dw, p.dwq_part, wave, p.D);
+}
+
+template <typename T, int LPR, int NM, bool FAR>
+__global__ __launch_bounds__(kWalkBlock) void bwd_k_pro(Params p, WalkCfg c) {
+  constexpr int VEC = VecOf<T>::value;
+  const int64_t wave = wave_id();
+  int b, hg, a;
+  const bool live = decode_tile(p, c, wave, b, hg, a);
+  const int lane = threadIdx.x & 63;
+  BwdKPro<T, LPR, NM, FAR> w;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) w.dw[e] = 0.f;
+  if (live) {
+    const int h = hg * (64 / LPR) + lane / LPR;
+    w.init(p, lane % LPR);
+    auto base = [&](const View& vw) {
+      return reinterpret_cast<const T*>(vw.p) + (int64_t)b * vw.sb + (int64_t)h * vw.sh;
+    };
+    w.q = base(p.q);
+    w.k = base(p.k);
+    w.go = base(p.dout);
+    w.dk = reinterpret_cast<T*>(p.dk.p) + (int64_t)b * p.dk.sb + (int64_t)h * p.dk.sh;
+    w.dv = reinterpret_cast<T*>(p.dv.p) + (int64_t)b * p.dv.sb + (int64_t)h * p.dv.sh;
+    w.qst = p.q.st;
+    w.kst = p.k.st;
+    w.gst = p.dout.st;
+    w.dkst = p.dk.st;
+    w.dvst = p.dv.st;
+    w.tab = p.tab + ((int64_t)b * p.T * p.H + h) * (2 * w.NS);
+    w.tst = (int64_t)p.H * 2 * w.NS;
+    w.F = c.F;
+    w.a = a;
+    w.end = min(a + c.P, p.T);
+    w.T_ = p.T;
+    // Walk u = a .. end+1 (slot of u is (u - a) & 3); key u - 2 is finished at step u.
+    walk4(w, a, w.end + 1);
+  }
+  write_wave_partial<T, LPR, true>(w.dw, p.dwk_part, wave, p.D);
+}
+
 // ================================================================= dispatch
 
 struct Pattern {
@@ -1015,14 +1506,18 @@ hipError_t launch_pattern(const Params& p, const WalkCfg& c, const Pattern& pat,
   const dim3 grid((unsigned)c.nwg), block(kWalkBlock);
 #define SBDA_WALK_CASE(NMV, FARV)                                                            \
   if (pat.nm == NMV && (pat.far != 0) == FARV) {                                             \
-    if (FWD && PRO)                                                                          \
-      hipLaunchKernelGGL((fwd_walk<T, LPR, NMV, FARV, true>), grid, block, 0, st, p, c);    \
-    else if (FWD)                                                                            \
+    if (FWD && PRO) {                                                                        \
+      hipLaunchKernelGGL((fwd_pipe_pro<T, LPR, NMV, FARV>), grid, block, 0, st, p, c);      \
+    } else if (FWD) {                                                                        \
       hipLaunchKernelGGL((fwd_pipe<T, LPR, NMV, FARV>), grid, block, 0, st, p, c);          \
-    else if (PRO)                                                                            \
-      hipLaunchKernelGGL((bwd_walk<T, LPR, NMV, FARV, true>), grid, block, 0, st, p, c);    \
-    else                                                                                     \
+    } else if (PRO) {                                                                        \
+      hipLaunchKernelGGL((bwd_q_pro<T, LPR, NMV, FARV>), grid, block, 0, st, p, c);         \
+      hipError_t e_ = hipGetLastError();                                                     \
+      if (e_ != hipSuccess) return e_;                                                       \
+      hipLaunchKernelGGL((bwd_k_pro<T, LPR, NMV, FARV>), grid, block, 0, st, p, c);         \
+    } else {                                                                                 \
       hipLaunchKernelGGL((bwd_pipe<T, LPR, NMV, FARV>), grid, block, 0, st, p, c);          \
+    }                                                                                        \
     return hipGetLastError();                                                                \
   }
   SBDA_WALK_CASE(3, false)
@@ -1084,12 +1579,13 @@ hipError_t walk_backward(const Params& p, int dtype, bool pro, hipStream_t st) {
   return walk_launch<false>(p, dtype, pro, st);
 }
 
-void walk_partials(const Params& p, int dtype, int64_t* pq, int64_t* pk) {
+void walk_partials(const Params& p, int dtype, int64_t* pq, int64_t* pk, int64_t* tab_floats) {
   Pattern pat;
   classify(p, &pat);
   const WalkCfg c = make_cfg(p, walk_lpr(p, dtype), pat);
   *pq = (int64_t)c.nwg * kWaves;
   *pk = *pq;
+  *tab_floats = (int64_t)p.B * p.T * p.H * 2 * p.S;
 }
 
 }  // namespace sbda

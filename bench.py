@@ -149,6 +149,22 @@ def other_configs(torch, sbda, dev) -> dict:
         "ms_per_step": ms, "positions_per_s": b * t / (ms * 1e-3),
         "algorithmic_gbs": (fwd_b + bwd_b) * 15 / (ms * 1e-3) / 1e9,
         "note": "B=4 T=32768 H=8 D=64 bf16, 15 layers, norm+RoPE fused, via autograd"}
+    del q, k, v, go
+    torch.cuda.empty_cache()
+    # Config 5: the SBDA backbone's forward_hidden (20 layers, d_model 512,
+    # 8 x 64 heads, FFN 2048, pre-RMSNorm, bf16, random init, vocab head
+    # excluded) on T=2^20 character ids.
+    cfg = sbda.BiAttnConfig(vocab_size=256, dim=512, layers=20, heads=8, ff_hidden=2048)
+    model = sbda.BiAttnLM(cfg).to(device=dev, dtype=torch.bfloat16).eval()
+    ids = torch.randint(0, 256, (1, 1 << 20), generator=gen, device=dev)
+    with torch.inference_mode():
+        ms = _median_ms(torch, lambda: model.forward_hidden(ids), reps=3)
+    res["config5_backbone_forward_hidden"] = {
+        "ms": ms, "tokens_per_s": (1 << 20) / (ms * 1e-3),
+        "note": "BiAttnLM.forward_hidden, 20 layers, d=512, 8x64 heads, FFN 2048, bf16, "
+                "T=2^20, vocab head excluded; attention = fused norm+RoPE+SBDA kernels, "
+                "projections/FFN = torch (hipBLASLt)"}
+    del model, ids
     return res
 
 

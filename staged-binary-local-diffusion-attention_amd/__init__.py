@@ -23,10 +23,11 @@ from .sbda import (
 )
 from .topology import PATH_TOPOLOGIES, sbda_stage, topology_offsets
 from .attention import BinaryPathAttention, SBDAAttention, SBDAttention
+from .model import BiAttnBlock, BiAttnConfig, BiAttnLM
 from ._lib import LIBRARY_PATH, SBDALibraryError
 
 __all__ = [
-    "BinaryPathAttention", "LIBRARY_PATH", "PATH_TOPOLOGIES", "SBDAAttention",
+    "BiAttnBlock", "BiAttnConfig", "BiAttnLM", "BinaryPathAttention", "LIBRARY_PATH", "PATH_TOPOLOGIES", "SBDAAttention",
     "SBDALibraryError", "SBDAttention", "fused_sbda", "fused_sbda_block",
     "fused_sbda_block_full", "fused_sbda_gqa_key_backward", "fused_sbda_key_backward",
     "fused_sbda_prologue", "host_offsets", "rope_inverse_frequencies", "rope_tables",

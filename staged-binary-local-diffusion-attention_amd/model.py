@@ -1,0 +1,208 @@
+"""Backbone counterpart of ``BiAttn/model.py`` for the SBDA backend.
+
+The caller of the fused attention: ``BiAttnConfig``, ``BiAttnBlock`` and
+``BiAttnLM`` keep the reference's names, config fields, defaults (except the
+backend, see below), parameter names and weight initialisation
+(``BiAttn/model.py:18-59,151-247,248-502``), with every attention layer an
+:class:`SBDAttention` that runs norm + RoPE + attention as one HIP op.
+
+Only what the SBDA route uses is here: ``attention_backend`` must be
+``"sbda"`` (the default in this mirror), the feed-forward is the dense SwiGLU,
+token IO is a plain (tied) embedding.  The reference's other backends, the
+DeepSeekMoE feed-forward, factorized token IO and ``path_active`` raise
+``ValueError``/``NotImplementedError``.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+from torch import Tensor, nn
+from torch.nn import functional as F
+
+from .attention import SBDAttention
+
+
+class RMSNorm(nn.Module):
+    """``BiAttn/model.py:18-29``."""
+
+    def __init__(self, dim: int, eps: float = 1e-6) -> None:
+        super().__init__()
+        self.dim = dim
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim))
+
+    def forward(self, x: Tensor) -> Tensor:
+        return F.rms_norm(x, (self.dim,), self.weight, self.eps)
+
+
+class SwiGLU(nn.Module):
+    """``BiAttn/model.py:32-59``: width ``ceil(dim * pi / 64) * 64`` unless given."""
+
+    def __init__(self, dim: int, ff_mult: float, dropout: float = 0.0, *,
+                 hidden_size: int | None = None, bias: bool = True) -> None:
+        super().__init__()
+        hidden = (max(64, math.ceil(dim * math.pi / 64) * 64)
+                  if hidden_size is None else hidden_size)
+        if hidden < 1:
+            raise ValueError("SwiGLU hidden_size must be positive")
+        self.hidden_size = hidden
+        self.gate = nn.Linear(dim, hidden, bias=bias)
+        self.up = nn.Linear(dim, hidden, bias=bias)
+        self.down = nn.Linear(hidden, dim, bias=bias)
+        self.dropout = nn.Dropout(dropout)
+
+    def forward(self, x: Tensor) -> Tensor:
+        return self.dropout(self.down(F.silu(self.gate(x)) * self.up(x)))
+
+
+@dataclass
+class BiAttnConfig:
+    """The reference's config fields that the SBDA route reads (``model.py:151-247``)."""
+
+    vocab_size: int
+    dim: int = 128
+    layers: int = 12
+    heads: int = 4
+    kv_heads: int | None = None
+    rope_theta: float = 1_000_000.0
+    ff_mult: float = 2.0
+    ff_hidden: int | None = None
+    ff_bias: bool = False
+    ff_mode: str = "dense"
+    dropout: float = 0.0
+    tie_embeddings: bool = True
+    attention_backend: str = "sbda"
+    path_sdpa: bool = True
+    sbda_fused: bool = True
+    sbda_backward: str = "key"
+    token_emb_dim: int | None = None
+
+    def window_schedule(self) -> tuple[int, ...]:
+        return tuple(2 ** (index + 1) for index in range(self.layers))
+
+    def validate(self) -> None:
+        if self.vocab_size <= 0 or self.dim <= 0 or self.layers <= 0:
+            raise ValueError("vocab_size, dim, and layers must be positive")
+        if self.attention_backend != "sbda":
+            raise ValueError("this backbone mirrors the sbda attention backend only")
+        if self.heads <= 0 or self.dim % self.heads:
+            raise ValueError("dim must be divisible by heads")
+        kv_heads = self.heads if self.kv_heads is None else self.kv_heads
+        if kv_heads <= 0 or self.heads % kv_heads:
+            raise ValueError("heads must be divisible by kv_heads")
+        if self.rope_theta <= 0:
+            raise ValueError("rope_theta must be positive")
+        if self.ff_mult <= 0 or not 0 <= self.dropout < 1:
+            raise ValueError("ff_mult must be positive and dropout in [0, 1)")
+        if self.ff_mode != "dense":
+            raise ValueError("only the dense SwiGLU feed-forward is mirrored")
+        if self.sbda_backward not in ("token", "block", "key"):
+            raise ValueError("sbda_backward must be token, block, or key")
+        if self.ff_hidden is not None and self.ff_hidden <= 0:
+            raise ValueError("ff_hidden must be positive when provided")
+        if self.token_emb_dim is not None:
+            raise ValueError("factorized token IO is not mirrored")
+
+
+class BiAttnBlock(nn.Module):
+    """Pre-norm block: ``x + attn(norm1(x))``, then ``+ ff(norm2(x))`` masked
+    by ``valid_mask`` (``BiAttn/model.py:248-335``)."""
+
+    def __init__(self, config: BiAttnConfig, layer_index: int) -> None:
+        super().__init__()
+        self.layer_index = int(layer_index)
+        self.norm1 = RMSNorm(config.dim)
+        self.attn = SBDAttention(
+            config.dim, config.heads, layer=layer_index + 1, kv_heads=config.kv_heads,
+            rope_theta=config.rope_theta, total_layers=config.layers,
+            use_sdpa=config.path_sdpa, use_fused=config.sbda_fused,
+            backward_mode=config.sbda_backward)
+        self.norm2 = RMSNorm(config.dim)
+        self.ff = SwiGLU(config.dim, config.ff_mult, config.dropout,
+                         hidden_size=config.ff_hidden, bias=config.ff_bias)
+
+    def forward(self, x: Tensor, valid_mask: Optional[Tensor],
+                seam_reset: Optional[Tensor] = None, path_indices: Optional[Tensor] = None,
+                path_valid: Optional[Tensor] = None) -> Tensor:
+        layer_paths = None if path_indices is None else path_indices[:, self.layer_index]
+        layer_valid = None if path_valid is None else path_valid[:, self.layer_index]
+        x = x + self.attn(self.norm1(x), valid_mask, seam_reset, layer_paths, layer_valid)
+        ff = self.ff(self.norm2(x))
+        if valid_mask is not None:
+            ff = ff * valid_mask[:, :, None].to(x.dtype)
+        return x + ff
+
+
+class BiAttnLM(nn.Module):
+    """Character LM backbone (``BiAttn/model.py:338-502``), SBDA layers only."""
+
+    def __init__(self, config: BiAttnConfig) -> None:
+        super().__init__()
+        config.validate()
+        self.config = config
+        self.embedding = nn.Embedding(config.vocab_size, config.dim)
+        self.drop = nn.Dropout(config.dropout)
+        self.layers = nn.ModuleList(BiAttnBlock(config, i) for i in range(config.layers))
+        self.norm = RMSNorm(config.dim)
+        self.lm_head = nn.Linear(config.dim, config.vocab_size, bias=False)
+        if config.tie_embeddings:
+            self.lm_head.weight = self.embedding.weight
+        self.apply(self._init_weights)
+
+    @staticmethod
+    def _init_weights(module: nn.Module) -> None:
+        if isinstance(module, nn.Linear):
+            nn.init.normal_(module.weight, mean=0.0, std=0.02)
+            if module.bias is not None:
+                nn.init.zeros_(module.bias)
+        elif isinstance(module, nn.Embedding):
+            nn.init.normal_(module.weight, mean=0.0, std=0.02)
+        elif isinstance(module, RMSNorm):
+            nn.init.ones_(module.weight)
+
+    def forward_hidden(self, input_ids: Tensor, valid_mask: Optional[Tensor] = None,
+                       seam_reset: Optional[Tensor] = None,
+                       path_indices: Optional[Tensor] = None,
+                       path_valid: Optional[Tensor] = None,
+                       path_active: Optional[Tensor] = None) -> Tensor:
+        """Final hidden states before the vocabulary projection."""
+        if input_ids.ndim != 2:
+            raise ValueError("input_ids must have shape [batch, sequence]")
+        if valid_mask is not None and (valid_mask.shape != input_ids.shape
+                                       or valid_mask.dtype != torch.bool):
+            raise ValueError("valid_mask must be bool with input_ids shape")
+        if path_active is not None:
+            raise NotImplementedError("path_active is not supported by the SBDA-AMD backbone")
+        # An all-true mask is dropped once here (model.py:439-440).
+        if valid_mask is not None and bool(valid_mask.all()):
+            valid_mask = None
+        x = self.drop(self.embedding(input_ids))
+        for layer in self.layers:
+            x = layer(x, valid_mask, seam_reset, path_indices, path_valid)
+        return self.norm(x)
+
+    def forward(self, input_ids: Tensor, valid_mask: Optional[Tensor] = None,
+                seam_reset: Optional[Tensor] = None, path_indices: Optional[Tensor] = None,
+                path_valid: Optional[Tensor] = None,
+                path_active: Optional[Tensor] = None) -> Tensor:
+        return self.lm_head(self.forward_hidden(input_ids, valid_mask, seam_reset,
+                                                path_indices, path_valid, path_active))
+
+    def next_logits(self, input_ids: Tensor, valid_mask: Tensor) -> Tensor:
+        """One logit vector per row, at its last valid token."""
+        hidden = self.forward_hidden(input_ids, valid_mask)
+        lengths = valid_mask.sum(dim=1) - 1
+        rows = torch.arange(input_ids.shape[0], device=input_ids.device)
+        return self.lm_head(hidden[rows, lengths])
+
+    def triangle_loss(self, input_ids: Tensor, valid_mask: Tensor, targets: Tensor) -> Tensor:
+        if targets.ndim != 1 or targets.shape[0] != input_ids.shape[0]:
+            raise ValueError("targets must contain one next token per triangle row")
+        return F.cross_entropy(self.next_logits(input_ids, valid_mask), targets)
+
+
+__all__ = ["BiAttnBlock", "BiAttnConfig", "BiAttnLM", "RMSNorm", "SwiGLU"]

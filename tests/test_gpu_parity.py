@@ -365,3 +365,37 @@ def test_sbdattention_module_rejects_eager_only_inputs():
         m(x, holes)
     with pytest.raises(NotImplementedError, match="seam_reset"):
         m(x, None, torch.zeros(1, 8, dtype=torch.bool, device=DEV))
+
+
+def test_backbone_forward_backward_matches_oracle_composition():
+    # BiAttnLM with SBDA layers (the reference's caller, BiAttn/model.py:248-502)
+    # against the same weights run through the oracle module forward on the CPU.
+    torch.manual_seed(60)
+    cfg = sbda_amd.BiAttnConfig(vocab_size=64, dim=256, layers=5, heads=4, rope_theta=10000.0,
+                                ff_hidden=512)
+    m = sbda_amd.BiAttnLM(cfg)
+    ids = torch.randint(0, 64, (2, 300))
+    valid = torch.ones(2, 300, dtype=torch.bool)
+    valid[0, 280:] = False
+    md = m.to(DEV)
+    out = md(ids.to(DEV), valid.to(DEV))
+    out.float().square().mean().backward()
+    torch.cuda.synchronize()
+    mc = sbda_amd.BiAttnLM(cfg)
+    mc.load_state_dict({k_: v_.cpu() for k_, v_ in md.state_dict().items()})
+
+    def oracle_forward(model, input_ids, vm):
+        x = model.embedding(input_ids)
+        for blk in model.layers:
+            x = x + _oracle_module_forward(blk.attn, blk.norm1(x), vm)
+            ff = blk.ff(blk.norm2(x)) * vm[:, :, None].to(x.dtype)
+            x = x + ff
+        return model.lm_head(model.norm(x))
+
+    want = oracle_forward(mc, ids, valid)
+    want.float().square().mean().backward()
+    torch.testing.assert_close(out.detach().cpu(), want.detach(), rtol=1e-4, atol=1e-4)
+    for (name, p), (_, pc) in zip(md.named_parameters(), mc.named_parameters()):
+        scale = pc.grad.abs().max().item() + 1e-8
+        err = (p.grad.cpu() - pc.grad).abs().max().item()
+        assert err / scale < 1e-3, f"{name}: {err} vs scale {scale}"

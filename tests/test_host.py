@@ -125,3 +125,19 @@ def test_module_surface_matches_reference():
     with pytest.raises(ValueError):
         m(torch.randn(1, 5, 32))
     assert sbda_amd.SBDAAttention is sbda_amd.SBDAttention
+
+
+def test_backbone_surface_matches_reference():
+    cfg = sbda_amd.BiAttnConfig(vocab_size=32, layers=4, dim=64, heads=4)
+    assert cfg.window_schedule() == (2, 4, 8, 16)
+    m = sbda_amd.BiAttnLM(cfg)
+    assert isinstance(m.layers[0].attn, sbda_amd.SBDAttention)
+    assert m.layers[3].attn.offsets == (0, 1, 2, 8)
+    assert m.lm_head.weight is m.embedding.weight
+    names = {n for n, _ in m.named_parameters()}
+    assert "layers.0.attn.q_norm.weight" in names and "layers.0.ff.gate.weight" in names
+    assert m.layers[0].ff.hidden_size == 256          # ceil(64 * pi / 64) * 64
+    with pytest.raises(ValueError):
+        sbda_amd.BiAttnConfig(vocab_size=32, attention_backend="left").validate()
+    with pytest.raises(NotImplementedError, match="CPU tensor"):
+        m(torch.tensor([[1, 2, 3]]))

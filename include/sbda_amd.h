@@ -28,6 +28,15 @@
  *   sbda_rope_table         -> BiAttn/attention_common.py:13-22
  *                              (_rope_cos_sin), as a [T, D/2] device table.
  *
+ * Masks (seg_key): every entry point that runs attention takes an optional
+ * device int32 array seg_key[B, T] (contiguous).  NULL = no mask.  Otherwise
+ * a source j of query i counts only if seg_key[b,i] >= 0 and
+ * seg_key[b,j] == seg_key[b,i]: -1 marks a padded position (valid_mask
+ * false) and a new value starts a segment (seam_reset), the key being
+ * valid ? cumsum(seam_reset) : -1 (BiAttn/left_v2.py:329-405, the source
+ * masking of the eager route).  A row with no counted source writes zeros and
+ * lse = +inf.  Masked calls run the generic kernels.
+ *
  * Return codes: SBDA_OK, or an error whose text sbda_last_error() returns
  * (thread-local).  SBDA_ERR_VALUE maps to Python ValueError, SBDA_ERR_DTYPE to
  * TypeError, SBDA_ERR_RUNTIME (a HIP error) to RuntimeError -- the error
@@ -72,7 +81,7 @@ int sbda_forward(const void* q, const int64_t* q_strides,
                  int64_t batch, int64_t heads, int64_t kv_heads,
                  int64_t length, int64_t head_dim, int32_t dtype,
                  const int32_t* offsets, int32_t num_offsets,
-                 void* stream);
+                 const int32_t* seg_key, void* stream);
 
 /*
  * Backward from the forward's saved q, k, v and lse.  Writes dq, dk, dv (each
@@ -89,7 +98,7 @@ int sbda_backward(const void* q, const int64_t* q_strides,
                   int64_t batch, int64_t heads, int64_t kv_heads,
                   int64_t length, int64_t head_dim, int32_t dtype,
                   const int32_t* offsets, int32_t num_offsets,
-                  void* stream);
+                  const int32_t* seg_key, void* stream);
 
 /*
  * Forward with the head-RMSNorm + RoPE prologue fused: q_raw and k_raw are
@@ -107,12 +116,13 @@ int sbda_forward_prologue(const void* q_raw, const int64_t* q_strides,
                           int64_t batch, int64_t heads, int64_t kv_heads,
                           int64_t length, int64_t head_dim, int32_t dtype,
                           const int32_t* offsets, int32_t num_offsets,
-                          void* stream);
+                          const int32_t* seg_key, void* stream);
 
 /* Workspace bytes sbda_backward_prologue needs for these shapes (< 0: error). */
 int64_t sbda_backward_prologue_workspace(int64_t batch, int64_t heads, int64_t kv_heads,
                                          int64_t length, int64_t head_dim, int32_t dtype,
-                                         const int32_t* offsets, int32_t num_offsets);
+                                         const int32_t* offsets, int32_t num_offsets,
+                                         const int32_t* seg_key);
 
 /*
  * Backward of sbda_forward_prologue: gradients of the raw q/k, of v and of
@@ -134,7 +144,7 @@ int sbda_backward_prologue(const void* q_raw, const int64_t* q_strides,
                            int64_t batch, int64_t heads, int64_t kv_heads,
                            int64_t length, int64_t head_dim, int32_t dtype,
                            const int32_t* offsets, int32_t num_offsets,
-                           void* stream);
+                           const int32_t* seg_key, void* stream);
 
 /*
  * RoPE tables: cos/sin[t, i] = cos/sin(fl32(t * inv_freq[i])) for t < length,

@@ -294,3 +294,56 @@ def key_gather_backward(q: Tensor, k: Tensor, v: Tensor, dout: Tensor,
     dk = dk_full.view(b_, hkv, group, t_, d_).sum(2)
     dv = dv_full.view(b_, hkv, group, t_, d_).sum(2)
     return dq, dk, dv
+
+
+# --------------------------------------------------------------------------
+# Masked variants: valid_mask with holes and seam_reset segments
+# --------------------------------------------------------------------------
+
+def masked_source_valid(length: int, offsets: Sequence[int], valid_mask: Tensor | None,
+                        seam_reset: Tensor | None) -> tuple[Tensor, Tensor]:
+    """``(indices [T,S], source_valid [B,T,S])`` of ``left_v2.py:329-378``.
+
+    A source is valid when it is in range, (with ``valid_mask``) is itself a
+    valid position, and (with ``seam_reset``) lies in the query's segment,
+    segments being ``cumsum(seam_reset)``.  With ``valid_mask``, slot 0 of a
+    padded query row is forced valid (``:371``) so its softmax is finite.
+    """
+    idx, base = path_tables(length, offsets)
+    batch = (valid_mask if valid_mask is not None else seam_reset).shape[0]
+    s = idx.shape[1]
+    ib = idx.unsqueeze(0).expand(batch, -1, -1)
+    valid = base.unsqueeze(0).expand(batch, -1, -1).clone()
+    if valid_mask is not None:
+        valid &= valid_mask.unsqueeze(-1).expand(-1, -1, s).gather(1, ib)
+        if seam_reset is not None:
+            seg = seam_reset.to(torch.int64).cumsum(dim=1)
+            valid &= seg.unsqueeze(-1).expand(-1, -1, s).gather(1, ib) == seg[:, :, None]
+        valid[:, :, 0] |= ~valid_mask
+    elif seam_reset is not None:
+        seg = seam_reset.to(torch.int64).cumsum(dim=1)
+        valid &= seg.unsqueeze(-1).expand(-1, -1, s).gather(1, ib) == seg[:, :, None]
+    return idx, valid
+
+
+def gather_attention_masked(q: Tensor, k: Tensor, v: Tensor, offsets: Sequence[int],
+                            valid_mask: Tensor | None = None,
+                            seam_reset: Tensor | None = None) -> Tensor:
+    """Eager attention with the reference's mask semantics (``left_v2.py:313-405``),
+    ``[B, H, T, D]`` in and out (before the output projection and the final
+    ``valid_mask`` multiply)."""
+    if valid_mask is None and seam_reset is None:
+        return gather_attention(q, k, v, offsets)
+    b, h, t, d = q.shape
+    k = _expand_kv(k, h)
+    v = _expand_kv(v, h)
+    idx, valid = masked_source_valid(t, offsets, valid_mask, seam_reset)
+    s = idx.shape[1]
+    src = idx[None, None, :, :, None].expand(b, h, t, s, d)
+    kg = k.unsqueeze(3).expand(b, h, t, s, d).gather(2, src)
+    vg = v.unsqueeze(3).expand(b, h, t, s, d).gather(2, src)
+    invalid = ~valid[:, None]
+    scores = torch.matmul(q.unsqueeze(-2), kg.transpose(-1, -2)).squeeze(-2) * (d ** -0.5)
+    scores = scores.masked_fill(invalid, torch.finfo(scores.dtype).min)
+    weights = scores.softmax(dim=-1).masked_fill(invalid, 0.0)
+    return torch.matmul(weights.unsqueeze(-2), vg).squeeze(-2)

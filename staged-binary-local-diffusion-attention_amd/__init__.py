@@ -20,6 +20,7 @@ from .sbda import (
     rope_tables,
     sbda_backward,
     sbda_forward,
+    segment_keys,
 )
 from .topology import PATH_TOPOLOGIES, sbda_stage, topology_offsets
 from .attention import BinaryPathAttention, SBDAAttention, SBDAttention
@@ -27,9 +28,10 @@ from .model import BiAttnBlock, BiAttnConfig, BiAttnLM
 from ._lib import LIBRARY_PATH, SBDALibraryError
 
 __all__ = [
-    "BiAttnBlock", "BiAttnConfig", "BiAttnLM", "BinaryPathAttention", "LIBRARY_PATH", "PATH_TOPOLOGIES", "SBDAAttention",
-    "SBDALibraryError", "SBDAttention", "fused_sbda", "fused_sbda_block",
-    "fused_sbda_block_full", "fused_sbda_gqa_key_backward", "fused_sbda_key_backward",
-    "fused_sbda_prologue", "host_offsets", "rope_inverse_frequencies", "rope_tables",
-    "sbda_backward", "sbda_forward", "sbda_stage", "topology_offsets",
+    "BiAttnBlock", "BiAttnConfig", "BiAttnLM", "BinaryPathAttention", "LIBRARY_PATH",
+    "PATH_TOPOLOGIES", "SBDAAttention", "SBDALibraryError", "SBDAttention", "fused_sbda",
+    "fused_sbda_block", "fused_sbda_block_full", "fused_sbda_gqa_key_backward",
+    "fused_sbda_key_backward", "fused_sbda_prologue", "host_offsets",
+    "rope_inverse_frequencies", "rope_tables", "sbda_backward", "sbda_forward",
+    "sbda_stage", "segment_keys", "topology_offsets",
 ]

@@ -11,7 +11,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("libsbda_amd.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 OK, ERR_VALUE, ERR_DTYPE, ERR_RUNTIME = 0, 1, 2, 3
 _ERRORS = {ERR_VALUE: ValueError, ERR_DTYPE: TypeError, ERR_RUNTIME: RuntimeError}
@@ -25,24 +25,25 @@ _offs = ctypes.POINTER(ctypes.c_int32)
 _fptr = ctypes.c_void_p
 
 _SHAPE = [_i64, _i64, _i64, _i64, _i64, _i32, _offs, _i32]
+_SEG = _p            # const int32_t* seg_key (device, NULL = unmasked)
 
 # name -> (restype, argtypes); exactly the functions include/sbda_amd.h declares.
 SIGNATURES = {
     "sbda_abi_version": (ctypes.c_int, []),
     "sbda_last_error": (ctypes.c_char_p, []),
     "sbda_forward": (ctypes.c_int, [_p, _strides, _p, _strides, _p, _strides, _p, _strides,
-                                    _fptr, *_SHAPE, _p]),
+                                    _fptr, *_SHAPE, _SEG, _p]),
     "sbda_backward": (ctypes.c_int, [_p, _strides, _p, _strides, _p, _strides, _p, _strides,
                                      _fptr, _p, _strides, _p, _strides, _p, _strides,
-                                     *_SHAPE, _p]),
+                                     *_SHAPE, _SEG, _p]),
     "sbda_forward_prologue": (ctypes.c_int, [_p, _strides, _p, _strides, _p, _strides, _p,
                                              _strides, _fptr, _fptr, _fptr, _p, _p, _f32,
-                                             *_SHAPE, _p]),
-    "sbda_backward_prologue_workspace": (ctypes.c_int64, _SHAPE),
+                                             *_SHAPE, _SEG, _p]),
+    "sbda_backward_prologue_workspace": (ctypes.c_int64, [*_SHAPE, _SEG]),
     "sbda_backward_prologue": (ctypes.c_int, [_p, _strides, _p, _strides, _p, _strides, _p,
                                               _strides, _fptr, _fptr, _fptr, _p, _p, _f32,
                                               _p, _strides, _p, _strides, _p, _strides,
-                                              _fptr, _fptr, _p, _i64, *_SHAPE, _p]),
+                                              _fptr, _fptr, _p, _i64, *_SHAPE, _SEG, _p]),
     "sbda_rope_table": (ctypes.c_int, [_p, _p, ctypes.POINTER(ctypes.c_float), _i64, _i64, _p]),
 }
 

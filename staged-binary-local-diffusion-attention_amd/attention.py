@@ -9,11 +9,14 @@ parameter names (``q``, ``k``, ``v``, ``q_norm.weight``, ``k_norm.weight``,
 The fused route is the only route: projections run in PyTorch, then
 head-RMSNorm + RoPE + SBDA attention run as one HIP op
 (:func:`sbda.fused_sbda_prologue`), then the output projection and the
-``valid_mask`` multiply (``left_v2.py:295-305``).  Inputs the reference
-sends to its eager gather path instead -- masks with interior holes,
-``seam_reset``, caller-supplied ``path_indices``/``path_valid``, routes with
-other than two or four offsets, or a CPU tensor -- raise
-``NotImplementedError`` here rather than silently taking a slower path.
+``valid_mask`` multiply (``left_v2.py:295-305``).  Masks the reference sends
+to its eager gather path -- a ``valid_mask`` with interior holes and
+``seam_reset`` (``left_v2.py:329-378``) -- run in the same HIP op through a
+per-position segment key (:func:`sbda.segment_keys`).  What remains eager-only
+in the reference -- caller-supplied ``path_indices``/``path_valid``, routes
+with other than two or four offsets, ``use_fused``/``use_sdpa`` off, a CPU
+tensor -- raises ``NotImplementedError`` here rather than silently taking a
+slower path.
 """
 
 from __future__ import annotations
@@ -21,7 +24,7 @@ from __future__ import annotations
 import torch
 from torch import Tensor, nn
 
-from .sbda import fused_sbda_prologue
+from .sbda import fused_sbda_prologue, segment_keys
 from .topology import PATH_TOPOLOGIES, topology_offsets
 
 
@@ -107,10 +110,6 @@ class BinaryPathAttention(nn.Module):
             reasons.append("a CPU tensor")
         if not (self.use_fused and self.use_sdpa):
             reasons.append("use_fused/use_sdpa disabled")
-        if not prefix_mask:
-            reasons.append("a valid_mask with interior holes")
-        if seam_reset is not None:
-            reasons.append("seam_reset")
         if path_indices is not None or path_valid is not None:
             reasons.append("caller-supplied path tables")
         if len(self.offsets) not in (2, 4):
@@ -119,13 +118,16 @@ class BinaryPathAttention(nn.Module):
             raise NotImplementedError(
                 "SBDA-AMD runs only the reference's fused route; this call needs the eager "
                 "gather path because of " + ", ".join(reasons))
+        # A prefix mask needs no key: causal sources of a valid row are valid.
+        seg_key = None if prefix_mask and seam_reset is None else segment_keys(
+            valid_mask, seam_reset)
         q = self.q(x).view(batch, length, self.heads, self.head_dim)
         k = self.k(x).view(batch, length, self.kv_heads, self.head_dim)
         v = self.v(x).view(batch, length, self.kv_heads, self.head_dim)
         attended = fused_sbda_prologue(
             q.permute(0, 2, 1, 3), k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3),
             self._fused_offsets, self.q_norm.weight, self.k_norm.weight,
-            theta=self.rope_theta, eps=self.q_norm.eps)
+            theta=self.rope_theta, eps=self.q_norm.eps, seg_key=seg_key)
         out = self.out(attended.transpose(1, 2).reshape(batch, length, dim))
         if valid_mask is not None:
             out = out * valid_mask[:, :, None].to(dtype=out.dtype)

@@ -113,11 +113,13 @@ int forward_impl(bool pro, const void* q, const int64_t* qs, const void* k, cons
                  const void* v, const int64_t* vs, void* out, const int64_t* os, float* lse,
                  const float* wq, const float* wk, const float* rc, const float* rs, float eps,
                  int64_t batch, int64_t heads, int64_t kv_heads, int64_t length, int64_t head_dim,
-                 int32_t dtype, const int32_t* offsets, int32_t n, void* stream) {
+                 int32_t dtype, const int32_t* offsets, int32_t n, const int32_t* seg,
+                 void* stream) {
   g_error.clear();
   Params p;
   int rc_ = check_problem(batch, heads, kv_heads, length, head_dim, dtype, offsets, n, p);
   if (rc_) return rc_;
+  p.seg = seg;
   const int esz = esize(dtype);
   if ((rc_ = check_view("q", q, qs, esz, false, &p.q))) return rc_;
   if ((rc_ = check_view("k", k, ks, esz, false, &p.k))) return rc_;
@@ -156,11 +158,12 @@ int backward_impl(bool pro, const void* q, const int64_t* qs, const void* k, con
                   const int64_t* dks, void* dv, const int64_t* dvs, float* dwq, float* dwk,
                   void* ws, int64_t ws_bytes, int64_t batch, int64_t heads, int64_t kv_heads,
                   int64_t length, int64_t head_dim, int32_t dtype, const int32_t* offsets,
-                  int32_t n, void* stream) {
+                  int32_t n, const int32_t* seg, void* stream) {
   g_error.clear();
   Params p;
   int rc_ = check_problem(batch, heads, kv_heads, length, head_dim, dtype, offsets, n, p);
   if (rc_) return rc_;
+  p.seg = seg;
   const int esz = esize(dtype);
   if ((rc_ = check_view("q", q, qs, esz, false, &p.q))) return rc_;
   if ((rc_ = check_view("k", k, ks, esz, false, &p.k))) return rc_;
@@ -208,26 +211,28 @@ using namespace sbda;
 
 extern "C" {
 
-int sbda_abi_version(void) { return 3; }
+int sbda_abi_version(void) { return 4; }
 
 const char* sbda_last_error(void) { return g_error.c_str(); }
 
 int sbda_forward(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
                  const int64_t* vs, void* out, const int64_t* os, float* lse, int64_t batch,
                  int64_t heads, int64_t kv_heads, int64_t length, int64_t head_dim, int32_t dtype,
-                 const int32_t* offsets, int32_t n, void* stream) {
+                 const int32_t* offsets, int32_t n, const int32_t* seg_key, void* stream) {
   return forward_impl(false, q, qs, k, ks, v, vs, out, os, lse, nullptr, nullptr, nullptr, nullptr,
-                      0.f, batch, heads, kv_heads, length, head_dim, dtype, offsets, n, stream);
+                      0.f, batch, heads, kv_heads, length, head_dim, dtype, offsets, n, seg_key,
+                      stream);
 }
 
 int sbda_backward(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
                   const int64_t* vs, const void* dout, const int64_t* dos, const float* lse, void* dq,
                   const int64_t* dqs, void* dk, const int64_t* dks, void* dv, const int64_t* dvs,
                   int64_t batch, int64_t heads, int64_t kv_heads, int64_t length, int64_t head_dim,
-                  int32_t dtype, const int32_t* offsets, int32_t n, void* stream) {
+                  int32_t dtype, const int32_t* offsets, int32_t n, const int32_t* seg_key,
+                  void* stream) {
   return backward_impl(false, q, qs, k, ks, v, vs, dout, dos, lse, nullptr, nullptr, nullptr, nullptr,
                        0.f, dq, dqs, dk, dks, dv, dvs, nullptr, nullptr, nullptr, 0, batch, heads,
-                       kv_heads, length, head_dim, dtype, offsets, n, stream);
+                       kv_heads, length, head_dim, dtype, offsets, n, seg_key, stream);
 }
 
 int sbda_forward_prologue(const void* q, const int64_t* qs, const void* k, const int64_t* ks,
@@ -235,18 +240,21 @@ int sbda_forward_prologue(const void* q, const int64_t* qs, const void* k, const
                           float* lse, const float* wq, const float* wk, const float* rc,
                           const float* rs, float eps, int64_t batch, int64_t heads,
                           int64_t kv_heads, int64_t length, int64_t head_dim, int32_t dtype,
-                          const int32_t* offsets, int32_t n, void* stream) {
+                          const int32_t* offsets, int32_t n, const int32_t* seg_key,
+                          void* stream) {
   return forward_impl(true, q, qs, k, ks, v, vs, out, os, lse, wq, wk, rc, rs, eps, batch, heads,
-                      kv_heads, length, head_dim, dtype, offsets, n, stream);
+                      kv_heads, length, head_dim, dtype, offsets, n, seg_key, stream);
 }
 
 int64_t sbda_backward_prologue_workspace(int64_t batch, int64_t heads, int64_t kv_heads,
                                          int64_t length, int64_t head_dim, int32_t dtype,
-                                         const int32_t* offsets, int32_t n) {
+                                         const int32_t* offsets, int32_t n,
+                                         const int32_t* seg_key) {
   g_error.clear();
   Params p;
   int rc = check_problem(batch, heads, kv_heads, length, head_dim, dtype, offsets, n, p);
   if (rc) return -rc;
+  p.seg = seg_key;
   int64_t pq = 0, pk = 0, tab = 0;
   partials(p, dtype, &pq, &pk, &tab);
   return ((pq + pk) * p.D + tab) * (int64_t)sizeof(float);
@@ -259,10 +267,11 @@ int sbda_backward_prologue(const void* q, const int64_t* qs, const void* k, cons
                            const int64_t* dks, void* dv, const int64_t* dvs, float* dwq,
                            float* dwk, void* ws, int64_t ws_bytes, int64_t batch, int64_t heads,
                            int64_t kv_heads, int64_t length, int64_t head_dim, int32_t dtype,
-                           const int32_t* offsets, int32_t n, void* stream) {
+                           const int32_t* offsets, int32_t n, const int32_t* seg_key,
+                           void* stream) {
   return backward_impl(true, q, qs, k, ks, v, vs, dout, dos, lse, wq, wk, rc, rs, eps, dq, dqs, dk,
                        dks, dv, dvs, dwq, dwk, ws, ws_bytes, batch, heads, kv_heads, length, head_dim,
-                       dtype, offsets, n, stream);
+                       dtype, offsets, n, seg_key, stream);
 }
 
 int sbda_rope_table(float* rope_cos, float* rope_sin, const float* inv_freq, int64_t length,

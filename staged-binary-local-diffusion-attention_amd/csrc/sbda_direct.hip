@@ -48,6 +48,14 @@ __device__ inline void load_key(const Params& p, int b, int hk, int64_t t, int l
   }
 }
 
+// Segment-key check of source j for query i (true when no keys are given).
+__device__ inline bool same_segment(const Params& p, int b, int i, int j) {
+  if (p.seg == nullptr) return true;
+  const int32_t* key = p.seg + (int64_t)b * p.T;
+  const int32_t ki = key[i];
+  return ki >= 0 && key[j] == ki;
+}
+
 // Decodes a global row id into (b, t, h) with heads fastest.
 __device__ inline void decode_row(int64_t row, int heads, int T, int& b, int& t, int& h) {
   h = (int)(row % heads);
@@ -114,11 +122,12 @@ __global__ __launch_bounds__(kBlock) void fwd_direct(Params p) {
   for (int s = 0; s < kMaxSlots; ++s) {
     if (s < p.S) {
       const int j = t - p.off[s];
-      src[s] = j;
       float k[VEC];
       load_key<T, LPR, PRO>(p, b, hk, j >= 0 ? j : 0, li, k);
       const float d = row_sum<LPR>(dot_partial<VEC>(q, k)) * p.scale;
-      sc[s] = j >= 0 ? d : -INFINITY;
+      const bool ok = j >= 0 && same_segment(p, b, t, j);
+      src[s] = ok ? j : -1;
+      sc[s] = ok ? d : -INFINITY;
       m = fmaxf(m, sc[s]);
     }
   }
@@ -181,7 +190,8 @@ __device__ inline void query_side(const Params& p, int b, int i, int h, int hk, 
       load_row<T, PRO>(row_ptr<T>(p.v, b, hk, jc), li, p.D, v);
       const float sc = row_sum<LPR>(dot_partial<VEC>(q, k)) * p.scale;
       const float d = row_sum<LPR>(dot_partial<VEC>(go, v));
-      pp[s] = j >= 0 ? fast_exp(sc - lse) : 0.f;  // lse = +inf -> 0
+      const bool ok = j >= 0 && same_segment(p, b, i, j);
+      pp[s] = ok ? fast_exp(sc - lse) : 0.f;  // lse = +inf -> 0
       dp[s] = d;
       delta = __builtin_fmaf(pp[s], d, delta);
       if constexpr (WANT_K) {

@@ -35,6 +35,9 @@ struct Params {
   float* dwq_part;             // [parts, D] fp32 per-block partial sums
   float* dwk_part;
   float* tab;                  // prologue backward: per (row, slot) (p, scale * dS), fp32
+  // Optional segment keys [B, T] (row stride T): a source j of query i counts
+  // only if key[i] >= 0 and key[j] == key[i].  nullptr = no masking.
+  const int32_t* seg;
 };
 
 enum DType : int { kBF16 = 0, kFP16 = 1, kFP32 = 2 };

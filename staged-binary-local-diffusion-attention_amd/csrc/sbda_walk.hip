@@ -1565,7 +1565,7 @@ hipError_t walk_launch(const Params& p, int dtype, bool pro, hipStream_t st) {
 
 bool walk_applies(const Params& p, int dtype) {
   Pattern pat;
-  if (p.group != 1 || !classify(p, &pat)) return false;
+  if (p.group != 1 || p.seg != nullptr || !classify(p, &pat)) return false;
   const int lpr = walk_lpr(p, dtype);
   if (lpr == 0) return false;
   return p.H % (64 / lpr) == 0;

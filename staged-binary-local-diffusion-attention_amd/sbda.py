@@ -17,6 +17,11 @@ reference's other backward variants of the same maths
 ``fused_sbda_prologue`` additionally fuses the per-head RMSNorm and RoPE of
 ``BiAttn/left_v2.py:237-239`` into the kernels.
 
+Every op takes an optional ``seg_key`` (int32 ``[B, T]``, see
+:func:`segment_keys`): the source masking of the reference's eager route
+(``valid_mask`` holes and ``seam_reset`` segments, ``left_v2.py:329-378``)
+as one key per position.
+
 Errors follow the reference's classes (``sbda_triton.py:1295-1302``):
 ``RuntimeError`` for a non-GPU tensor, ``ValueError`` for shapes / source
 counts, ``TypeError`` for dtypes.  A missing library raises
@@ -105,6 +110,46 @@ def _shape_args(q, k, offs):
     return (b, h, k.shape[1], t, d, _DTYPES[q.dtype], _lib.offsets_array(offs), len(offs))
 
 
+def segment_keys(valid_mask: torch.Tensor | None,
+                 seam_reset: torch.Tensor | None) -> torch.Tensor | None:
+    """One int32 key per position (``[B, T]``, contiguous) encoding the
+    reference's source masks (``BiAttn/left_v2.py:329-378``).
+
+    The segment of a position is ``cumsum(seam_reset)`` along the sequence; a
+    position whose ``valid_mask`` is false gets ``-1``.  The kernels count a
+    source only when its key equals the query's and the query's key is not
+    ``-1``.  ``None`` when neither mask is given.
+
+    The reference forces slot 0 of a padded query row valid so its softmax is
+    finite (``left_v2.py:371``); here such a row has no source and returns
+    zeros.  Its output row is multiplied by ``valid_mask`` afterwards in both,
+    so module outputs and gradients agree.
+    """
+    if valid_mask is None and seam_reset is None:
+        return None
+    ref = valid_mask if valid_mask is not None else seam_reset
+    if ref.ndim != 2:
+        raise ValueError("masks must have shape [batch, sequence]")
+    if seam_reset is not None:
+        if seam_reset.shape != ref.shape:
+            raise ValueError("valid_mask and seam_reset must have one shape")
+        key = seam_reset.to(torch.int32).cumsum(dim=1, dtype=torch.int32)
+    else:
+        key = torch.zeros(ref.shape, dtype=torch.int32, device=ref.device)
+    if valid_mask is not None:
+        key = key.masked_fill(~valid_mask.to(torch.bool), -1)
+    return key.contiguous()
+
+
+def _seg_arg(seg_key: torch.Tensor | None, q: torch.Tensor) -> ctypes.c_void_p:
+    if seg_key is None:
+        return ctypes.c_void_p(0)
+    if (seg_key.dtype != torch.int32 or seg_key.device != q.device
+            or seg_key.shape != (q.shape[0], q.shape[2]) or not seg_key.is_contiguous()):
+        raise ValueError("seg_key must be a contiguous int32 [B, T] tensor on q's device")
+    return ctypes.c_void_p(seg_key.data_ptr())
+
+
 # -------------------------------------------------------- raw entry points
 
 def _lse_storage(b: int, h: int, t: int, device) -> torch.Tensor:
@@ -120,7 +165,7 @@ def _lse_buffer(lse: torch.Tensor) -> torch.Tensor:
     return buf if buf.is_contiguous() else buf.contiguous()
 
 
-def sbda_forward(q, k, v, offsets) -> tuple[torch.Tensor, torch.Tensor]:
+def sbda_forward(q, k, v, offsets, seg_key=None) -> tuple[torch.Tensor, torch.Tensor]:
     """Forward without autograd: ``(out [B,H,T,D], lse [B,H,T] fp32)``."""
     offs = host_offsets(offsets)
     _validate(q, k, v, offs, gqa=True)
@@ -132,11 +177,12 @@ def sbda_forward(q, k, v, offsets) -> tuple[torch.Tensor, torch.Tensor]:
     with torch.cuda.device(q.device):
         _lib.check(lib.sbda_forward(
             _ptr(q), _lib.strides(q), _ptr(k), _lib.strides(k), _ptr(v), _lib.strides(v),
-            _ptr(out), _lib.strides(out), _ptr(lse), *_shape_args(q, k, offs), _stream(q)))
+            _ptr(out), _lib.strides(out), _ptr(lse), *_shape_args(q, k, offs),
+            _seg_arg(seg_key, q), _stream(q)))
     return out, lse
 
 
-def sbda_backward(q, k, v, grad_out, lse, offsets):
+def sbda_backward(q, k, v, grad_out, lse, offsets, seg_key=None):
     """Backward without autograd: ``(dq, dk, dv)`` from saved ``lse``."""
     offs = host_offsets(offsets)
     _validate(q, k, v, offs, gqa=True)
@@ -153,7 +199,7 @@ def sbda_backward(q, k, v, grad_out, lse, offsets):
             _ptr(q), _lib.strides(q), _ptr(k), _lib.strides(k), _ptr(v), _lib.strides(v),
             _ptr(grad_out), _lib.strides(grad_out), _ptr(lse),
             _ptr(dq), _lib.strides(dq), _ptr(dk), _lib.strides(dk), _ptr(dv), _lib.strides(dv),
-            *_shape_args(q, k, offs), _stream(q)))
+            *_shape_args(q, k, offs), _seg_arg(seg_key, q), _stream(q)))
     return dq, dk, dv
 
 
@@ -163,29 +209,29 @@ class _FusedSBDAKeyBackward(torch.autograd.Function):
     """O + per-row LSE forward; gather-form, atomic-free backward."""
 
     @staticmethod
-    def forward(ctx, q, k, v, offsets):
-        out, lse = sbda_forward(q, k, v, offsets)
+    def forward(ctx, q, k, v, offsets, seg_key):
+        out, lse = sbda_forward(q, k, v, offsets, seg_key)
         ctx.save_for_backward(_kernel_view(q), _kernel_view(k), _kernel_view(v), lse)
-        ctx.offs = host_offsets(offsets)
+        ctx.offs, ctx.seg_key = host_offsets(offsets), seg_key
         return out
 
     @staticmethod
     def backward(ctx, grad_out):
         q, k, v, lse = ctx.saved_tensors
-        dq, dk, dv = sbda_backward(q, k, v, grad_out, lse, ctx.offs)
-        return dq, dk, dv, None
+        dq, dk, dv = sbda_backward(q, k, v, grad_out, lse, ctx.offs, ctx.seg_key)
+        return dq, dk, dv, None, None
 
 
-def fused_sbda_key_backward(q, k, v, offsets):
+def fused_sbda_key_backward(q, k, v, offsets, *, seg_key=None):
     """Fused SBDA attention, ``[B,H,T,D]`` in and out (``sbda_triton.py:1468-1475``)."""
     if k.shape != q.shape or v.shape != q.shape:
         raise ValueError("q, k, and v must have matching [B,H,L,D] shapes")
-    return _FusedSBDAKeyBackward.apply(q, k, v, offsets)
+    return _FusedSBDAKeyBackward.apply(q, k, v, offsets, seg_key)
 
 
-def fused_sbda_gqa_key_backward(q, k, v, offsets):
+def fused_sbda_gqa_key_backward(q, k, v, offsets, *, seg_key=None):
     """Fused SBDA with ``k``/``v`` at ``kv_heads`` (``sbda_triton.py:1477-1493``)."""
-    return _FusedSBDAKeyBackward.apply(q, k, v, offsets)
+    return _FusedSBDAKeyBackward.apply(q, k, v, offsets, seg_key)
 
 
 # The reference's token/block backward variants compute the same maths with
@@ -242,7 +288,7 @@ def _weight32(w: torch.Tensor, d: int, device) -> torch.Tensor:
 
 class _FusedSBDAPrologue(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q_raw, k_raw, v, q_weight, k_weight, offsets, theta, eps):
+    def forward(ctx, q_raw, k_raw, v, q_weight, k_weight, offsets, theta, eps, seg_key):
         offs = host_offsets(offsets)
         _validate(q_raw, k_raw, v, offs, gqa=True)
         lib = _lib.load()
@@ -256,9 +302,9 @@ class _FusedSBDAPrologue(torch.autograd.Function):
             _lib.check(lib.sbda_forward_prologue(
                 _ptr(q), _lib.strides(q), _ptr(k), _lib.strides(k), _ptr(v), _lib.strides(v),
                 _ptr(out), _lib.strides(out), _ptr(lse), _ptr(wq), _ptr(wk), _ptr(cos), _ptr(sin),
-                float(eps), *_shape_args(q, k, offs), _stream(q)))
+                float(eps), *_shape_args(q, k, offs), _seg_arg(seg_key, q), _stream(q)))
         ctx.save_for_backward(q, k, v, wq, wk, lse, cos, sin)
-        ctx.offs, ctx.eps = offs, float(eps)
+        ctx.offs, ctx.eps, ctx.seg_key = offs, float(eps), seg_key
         ctx.wdtypes = (q_weight.dtype, k_weight.dtype)
         return out
 
@@ -275,7 +321,8 @@ class _FusedSBDAPrologue(torch.autograd.Function):
         dwq = torch.empty(d, dtype=torch.float32, device=q.device)
         dwk = torch.empty_like(dwq)
         shape = _shape_args(q, k, offs)
-        need = lib.sbda_backward_prologue_workspace(*shape)
+        seg = _seg_arg(ctx.seg_key, q)
+        need = lib.sbda_backward_prologue_workspace(*shape, seg)
         if need < 0:
             _lib.check(-need)
         ws = torch.empty(max(int(need), 16), dtype=torch.uint8, device=q.device)
@@ -285,13 +332,13 @@ class _FusedSBDAPrologue(torch.autograd.Function):
                 _ptr(g), _lib.strides(g), _ptr(lse), _ptr(wq), _ptr(wk), _ptr(cos), _ptr(sin),
                 ctx.eps, _ptr(dq), _lib.strides(dq), _ptr(dk), _lib.strides(dk),
                 _ptr(dv), _lib.strides(dv), _ptr(dwq), _ptr(dwk), _ptr(ws), ws.numel(),
-                *shape, _stream(q)))
+                *shape, seg, _stream(q)))
         return (dq, dk, dv, dwq.to(ctx.wdtypes[0]), dwk.to(ctx.wdtypes[1]),
-                None, None, None)
+                None, None, None, None)
 
 
 def fused_sbda_prologue(q_raw, k_raw, v, offsets, q_weight, k_weight, *,
-                        theta: float, eps: float = 1e-6):
+                        theta: float, eps: float = 1e-6, seg_key=None):
     """Head-RMSNorm(q, k) -> RoPE -> SBDA attention in one fused op.
 
     ``q_raw``: ``[B, H, T, D]`` projections before normalisation; ``k_raw``,
@@ -300,12 +347,12 @@ def fused_sbda_prologue(q_raw, k_raw, v, offsets, q_weight, k_weight, *,
     v, offsets)`` with the reference's prologue (``BiAttn/left_v2.py:237-239``).
     """
     return _FusedSBDAPrologue.apply(q_raw, k_raw, v, q_weight, k_weight, offsets,
-                                    float(theta), float(eps))
+                                    float(theta), float(eps), seg_key)
 
 
 __all__ = [
     "fused_sbda", "fused_sbda_block", "fused_sbda_block_full",
     "fused_sbda_key_backward", "fused_sbda_gqa_key_backward",
     "fused_sbda_prologue", "host_offsets", "rope_inverse_frequencies", "rope_tables",
-    "sbda_backward", "sbda_forward",
+    "sbda_backward", "sbda_forward", "segment_keys",
 ]

@@ -308,16 +308,21 @@ def test_tile_edges_and_offset_patterns(t, offs):
 
 # ------------------------------------------------------------ module level
 
-def _oracle_module_forward(m, x, valid_mask=None):
-    """The reference module's fused-route forward (left_v2.py:234-306),
-    restated with the oracle's prologue and gather attention."""
+def _oracle_module_forward(m, x, valid_mask=None, seam_reset=None):
+    """The reference module's forward (left_v2.py:234-306 fused route, or the
+    eager masked gather of :313-405 for holes / seams), restated with the
+    oracle's prologue and gather attention."""
     b, t, dim = x.shape
     q = (x @ m.q.weight.T).view(b, t, m.heads, m.head_dim)
     k = (x @ m.k.weight.T).view(b, t, m.kv_heads, m.head_dim)
     v = (x @ m.v.weight.T).view(b, t, m.kv_heads, m.head_dim)
     q, k = ref.prologue(q, k, m.q_norm.weight, m.k_norm.weight, m.rope_theta)
-    att = ref.gather_attention(q.permute(0, 2, 1, 3), k.permute(0, 2, 1, 3),
-                               v.permute(0, 2, 1, 3), m.offsets)
+    qh, kh, vh = (x_.permute(0, 2, 1, 3) for x_ in (q, k, v))
+    prefix = valid_mask is None or bool(torch.all(~valid_mask[:, 1:] | valid_mask[:, :-1]))
+    if prefix and seam_reset is None:
+        att = ref.gather_attention(qh, kh, vh, m.offsets)
+    else:
+        att = ref.gather_attention_masked(qh, kh, vh, m.offsets, valid_mask, seam_reset)
     out = att.transpose(1, 2).reshape(b, t, dim) @ m.out.weight.T
     if valid_mask is not None:
         out = out * valid_mask[:, :, None].to(out.dtype)
@@ -360,11 +365,126 @@ def test_sbdattention_module_matches_oracle_module(layer, kv_heads):
 def test_sbdattention_module_rejects_eager_only_inputs():
     m = sbda_amd.SBDAttention(64, 4, 3).to(DEV)
     x = torch.randn(1, 8, 64, device=DEV)
-    holes = torch.tensor([[True, False, True, True, True, True, True, True]], device=DEV)
-    with pytest.raises(NotImplementedError, match="interior holes"):
-        m(x, holes)
-    with pytest.raises(NotImplementedError, match="seam_reset"):
-        m(x, None, torch.zeros(1, 8, dtype=torch.bool, device=DEV))
+    paths = torch.zeros(1, 8, 4, dtype=torch.long, device=DEV)
+    with pytest.raises(NotImplementedError, match="path tables"):
+        m(x, None, None, paths)
+    off = sbda_amd.SBDAttention(64, 4, 3, use_fused=False).to(DEV)
+    with pytest.raises(NotImplementedError, match="use_fused"):
+        off(x)
+
+
+# ------------------------------------------------------------ masks
+
+def _masks(b, t, seed):
+    """Holes, a padded tail and seams, the masks of left_v2.py:329-378."""
+    g = torch.Generator().manual_seed(seed)
+    valid = torch.rand(b, t, generator=g) > 0.15
+    valid[0, t - t // 5:] = False
+    seam = torch.rand(b, t, generator=g) < 0.03
+    seam[:, 0] = False
+    return valid, seam
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, FP32_TOL), (torch.bfloat16, LOW_TOL)])
+@pytest.mark.parametrize("offs,hkv,d", [((0, 1), None, 64), ((0, 1, 2, 4), None, 64),
+                                        ((0, 1, 2, 64), None, 64), ((0, 1, 2, 16), 2, 64),
+                                        ((0, 2), 4, 40), ((0, 1, 2, 128), None, 128)])
+@pytest.mark.parametrize("which", ["holes", "seams", "both"])
+def test_masked_op_matches_oracle(dtype, tol, offs, hkv, d, which):
+    b, t, h = 2, 300, 8
+    q, k, v, g = _inputs(b, t, h, d, dtype, seed=hash((offs, d, which)) % 1000, hkv=hkv)
+    valid, seam = _masks(b, t, seed=len(offs) * 7 + d)
+    vm = None if which == "seams" else valid
+    sr = None if which == "holes" else seam
+    keep = torch.ones(b, t, dtype=torch.bool) if vm is None else vm
+    g = g * keep[:, :, None, None].to(dtype)        # padded rows get no gradient
+    key = sbda_amd.segment_keys(None if vm is None else vm.to(DEV),
+                                None if sr is None else sr.to(DEV))
+    qd, kd, vd = (_dev(x).requires_grad_() for x in (q, k, v))
+    off = torch.tensor(offs, dtype=torch.int32, device=DEV)
+    out = sbda_amd.fused_sbda_gqa_key_backward(qd, kd, vd, off, seg_key=key)
+    out.backward(_dev(g))
+    torch.cuda.synchronize()
+    got = [x.detach().float().cpu() for x in (out, qd.grad, kd.grad, vd.grad)]
+    rq, rk, rv = (x.float().permute(0, 2, 1, 3).requires_grad_() for x in (q, k, v))
+    want = ref.gather_attention_masked(rq, rk, rv, offs, vm, sr)
+    want.backward(g.float().permute(0, 2, 1, 3))
+    rows = keep[:, None, :, None].expand_as(got[0])
+    # Padded query rows: zeros here, slot 0 forced valid in the reference;
+    # both are multiplied by valid_mask by the caller.
+    assert torch.all(got[0][~rows] == 0)
+    torch.testing.assert_close(got[0][rows], want.detach()[rows], **tol)
+    for name, a, r in zip(("dq", "dk", "dv"), got[1:], (rq.grad, rk.grad, rv.grad)):
+        torch.testing.assert_close(a, r, **tol, msg=lambda m: f"{which} {offs} {name}: {m}")
+
+
+def test_masked_prologue_matches_unmasked_on_independent_segments():
+    # seam_reset splits a batch row into segments that attend as separate
+    # sequences would (RoPE positions stay global): the second segment's
+    # results must not change when everything before the seam does, and the
+    # first segment's must equal the unmasked op on the prefix.
+    b, t, h, d = 1, 512, 8, 64
+    q, k, v, g = _inputs(b, t, h, d, torch.bfloat16, seed=91)
+    offs = (0, 1, 2, 32)
+    seam = torch.zeros(b, t, dtype=torch.bool)
+    seam[0, 256] = True
+    wq = (1 + 0.1 * torch.randn(d)).to(DEV)
+    wk = (1 + 0.1 * torch.randn(d)).to(DEV)
+    off = torch.tensor(offs, dtype=torch.int32, device=DEV)
+    key = sbda_amd.segment_keys(None, seam.to(DEV))
+
+    def run(seg_key, qx, kx, vx, gx):
+        qd, kd, vd = (_dev(x).requires_grad_() for x in (qx, kx, vx))
+        out = sbda_amd.fused_sbda_prologue(qd, kd, vd, off, wq, wk, theta=10000.0,
+                                           seg_key=seg_key)
+        out.backward(_dev(gx))
+        torch.cuda.synchronize()
+        return [x.detach().float().cpu() for x in (out, qd.grad, kd.grad, vd.grad)]
+
+    masked = run(key, q, k, v, g)
+    # Second segment alone: the first segment's k/v replaced by values that
+    # would change every result if any of them were read as a source.
+    k2, v2 = k.clone(), v.clone()
+    k2[:, :256] = 50.0
+    v2[:, :256] = -50.0
+    second = run(key, q, k2, v2, g)
+    for a, bb in zip(masked, second):
+        torch.testing.assert_close(a[:, :, 256:], bb[:, :, 256:], rtol=0, atol=0)
+    # and the first segment equals the unmasked op cut at the seam (another
+    # kernel family, so within the bf16 tolerance rather than bit for bit).
+    plain = run(None, q[:, :256], k[:, :256], v[:, :256], g[:, :256])
+    for a, bb in zip(masked, plain):
+        torch.testing.assert_close(a[:, :, :256], bb, **LOW_TOL)
+
+
+@pytest.mark.parametrize("layer", [3, 8])
+def test_sbdattention_module_with_holes_and_seams_matches_oracle(layer):
+    torch.manual_seed(70 + layer)
+    dim, heads, t = 256, 4, 400
+    m = sbda_amd.SBDAttention(dim, heads, layer, rope_theta=10000.0, total_layers=12)
+    with torch.no_grad():
+        m.q_norm.weight.mul_(1 + 0.1 * torch.randn(m.head_dim))
+        m.k_norm.weight.mul_(1 + 0.1 * torch.randn(m.head_dim))
+    x = torch.randn(2, t, dim)
+    valid, seam = _masks(2, t, seed=layer)
+    g = torch.randn(2, t, dim)
+    md = m.to(DEV)
+    xd = x.to(DEV).requires_grad_()
+    out = md(xd, valid.to(DEV), seam.to(DEV))
+    out.backward(g.to(DEV))
+    torch.cuda.synchronize()
+    mc = sbda_amd.SBDAttention(dim, heads, layer, rope_theta=10000.0, total_layers=12)
+    mc.load_state_dict({k_: v_.cpu() for k_, v_ in md.state_dict().items()})
+    xc = x.clone().requires_grad_()
+    want = _oracle_module_forward(mc, xc, valid, seam)
+    want.backward(g)
+    tol = dict(rtol=1e-4, atol=1e-4)
+    torch.testing.assert_close(out.detach().cpu(), want.detach(), **tol)
+    torch.testing.assert_close(xd.grad.cpu(), xc.grad, **tol)
+    for (name, p), (_, pc) in zip(md.named_parameters(), mc.named_parameters()):
+        scale = pc.grad.abs().max().item() + 1e-6
+        err = (p.grad.cpu() - pc.grad).abs().max().item()
+        assert err / scale < 1e-4, f"{name}: {err} vs scale {scale}"
 
 
 def test_backbone_forward_backward_matches_oracle_composition():

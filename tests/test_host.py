@@ -44,7 +44,7 @@ def _shape_call(lib, **kw):
     offs = args["offsets"]
     return lib.sbda_backward_prologue_workspace(
         args["batch"], args["heads"], args["kv_heads"], args["length"], args["head_dim"],
-        args["dtype"], _lib.offsets_array(offs), len(offs))
+        args["dtype"], _lib.offsets_array(offs), len(offs), None)
 
 
 def test_validation_errors_without_launching():
@@ -61,7 +61,7 @@ def test_validation_errors_without_launching():
     z = ctypes.c_void_p(0)
     st = (ctypes.c_int64 * 4)(0, 0, 0, 1)
     rc = lib.sbda_forward(z, st, z, st, z, st, z, st, z, 1, 1, 1, 8, 64, 0,
-                          _lib.offsets_array((0, 1)), 2, z)
+                          _lib.offsets_array((0, 1)), 2, z, z)
     assert rc == _lib.ERR_VALUE and "null" in lib.sbda_last_error().decode()
     with pytest.raises(ValueError):
         _lib.check(_lib.ERR_VALUE)
@@ -73,6 +73,30 @@ def test_python_op_rejects_cpu_tensors_like_the_reference():
     q = torch.zeros(1, 2, 8, 64)
     with pytest.raises(RuntimeError):
         sbda_amd.fused_sbda_key_backward(q, q, q, torch.tensor([0, 1], dtype=torch.int32))
+
+
+def test_segment_keys_encode_the_reference_masks():
+    valid = torch.tensor([[True, True, False, True, True], [True, True, True, True, True]])
+    seam = torch.tensor([[False, False, False, True, False], [False, True, False, False, True]])
+    assert sbda_amd.segment_keys(None, None) is None
+    assert sbda_amd.segment_keys(valid, None).tolist() == [[0, 0, -1, 0, 0], [0] * 5]
+    assert sbda_amd.segment_keys(None, seam).tolist() == [[0, 0, 0, 1, 1], [0, 1, 1, 1, 2]]
+    keys = sbda_amd.segment_keys(valid, seam)
+    assert keys.dtype == torch.int32 and keys.is_contiguous()
+    assert keys.tolist() == [[0, 0, -1, 1, 1], [0, 1, 1, 1, 2]]
+    # The key test "key[j] == key[i] >= 0" is the oracle's source-valid table
+    # for every valid query row (padded rows differ only in the forced slot 0).
+    offs = (0, 1, 2, 4)
+    idx, ok = ref.masked_source_valid(5, offs, valid, seam)
+    in_range = torch.tensor([[i - o >= 0 for o in offs] for i in range(5)])
+    for b in range(2):
+        for i in range(5):
+            if not valid[b, i]:
+                continue
+            for s in range(4):
+                mine = bool(in_range[i, s]) and keys[b, i] >= 0 and \
+                    keys[b, int(idx[i, s])] == keys[b, i]
+                assert mine == bool(ok[b, i, s]), (b, i, s)
 
 
 def test_host_offsets_cache():

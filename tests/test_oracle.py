@@ -288,3 +288,57 @@ def test_planted_mistakes_are_caught():
     # A dropped softmax scale or a transposed (k <-> v) operand also differs.
     assert not torch.allclose(ref.gather_attention(q * 8, k, v, offs), want, atol=1e-6)
     assert not torch.allclose(ref.gather_attention(q, v, k, offs), want, atol=1e-6)
+
+
+# ----------------------------------------------------------------- masks
+
+def test_seam_reset_equals_independent_segments():
+    # A seam at position s makes [0, s) and [s, T) two independent sequences:
+    # the masked attention on the whole equals plain attention on each part.
+    t, s_ = 23, 9
+    q, k, v = (_rand(1, 2, t, 4, seed=s) for s in (60, 61, 62))
+    seam = torch.zeros(1, t, dtype=torch.bool)
+    seam[0, 0] = True
+    seam[0, s_] = True
+    for offs in ((0, 1), (0, 1, 2, 4), (0, 1, 2, 16)):
+        got = ref.gather_attention_masked(q, k, v, offs, seam_reset=seam)
+        left = ref.gather_attention(q[:, :, :s_], k[:, :, :s_], v[:, :, :s_], offs)
+        right = ref.gather_attention(q[:, :, s_:], k[:, :, s_:], v[:, :, s_:], offs)
+        torch.testing.assert_close(got, torch.cat((left, right), dim=2), rtol=1e-12, atol=1e-12)
+
+
+def test_holes_are_skipped_and_prefix_masks_change_nothing():
+    t = 17
+    offs = (0, 1, 2, 8)
+    q, k, v = (_rand(2, 2, t, 4, seed=s) for s in (63, 64, 65))
+    prefix = torch.ones(2, t, dtype=torch.bool)
+    prefix[1, 12:] = False
+    got = ref.gather_attention_masked(q, k, v, offs, valid_mask=prefix)
+    plain = ref.gather_attention(q, k, v, offs)
+    # Causal sources of a valid query are valid under a prefix mask.
+    torch.testing.assert_close(got[1, :, :12], plain[1, :, :12], rtol=0, atol=0)
+    torch.testing.assert_close(got[0], plain[0], rtol=0, atol=0)
+    holes = torch.ones(1, t, dtype=torch.bool)
+    holes[0, 5] = False
+    h_out = ref.gather_attention_masked(q[:1], k[:1], v[:1], offs, valid_mask=holes)
+    # Brute force: drop source 5 from every query's softmax.
+    for i in range(t):
+        if not holes[0, i]:
+            continue
+        srcs = [i - o for o in offs if o <= i and i - o != 5]
+        for hh in range(2):
+            sc = torch.stack([(q[0, hh, i] * k[0, hh, j]).sum() / 2 for j in srcs])
+            w = torch.softmax(sc, 0)
+            want = sum(w[n] * v[0, hh, j] for n, j in enumerate(srcs))
+            torch.testing.assert_close(h_out[0, hh, i], want, rtol=1e-12, atol=1e-12)
+
+
+def test_masked_gradcheck_fp64():
+    t = 9
+    valid = torch.ones(1, t, dtype=torch.bool)
+    valid[0, 3] = False
+    seam = torch.zeros(1, t, dtype=torch.bool)
+    seam[0, 6] = True
+    q, k, v = (_rand(1, 2, t, 3, seed=s).requires_grad_() for s in (66, 67, 68))
+    assert torch.autograd.gradcheck(
+        lambda a, b, c: ref.gather_attention_masked(a, b, c, (0, 1, 2, 4), valid, seam), (q, k, v))

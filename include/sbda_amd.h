@@ -37,6 +37,16 @@
  * masking of the eager route).  A row with no counted source writes zeros and
  * lse = +inf.  Masked calls run the generic kernels.
  *
+ * Source tables (sbda_forward_paths / sbda_backward_paths): instead of the
+ * layer's offsets, query i of batch b reads the sources path_indices[b,i,s]
+ * (device int64 [B, T, S], contiguous, any S >= 1); source s counts when
+ * path_valid[b,i,s] != 0 (device bytes, e.g. a torch.bool tensor; NULL = all),
+ * 0 <= j <= i, and the segment keys agree.  This is the eager route of
+ * BiAttn/left_v2.py:212-231,313-378 (tables produced for the greedy H4 schedule,
+ * BinaryDiffusionAttention/run_mini_experiment.py:117-133).  The fused norm +
+ * RoPE prologue is on when q_weight/k_weight/rope_cos/rope_sin are given (all
+ * four) and off when all four are NULL.
+ *
  * Return codes: SBDA_OK, or an error whose text sbda_last_error() returns
  * (thread-local).  SBDA_ERR_VALUE maps to Python ValueError, SBDA_ERR_DTYPE to
  * TypeError, SBDA_ERR_RUNTIME (a HIP error) to RuntimeError -- the error
@@ -145,6 +155,53 @@ int sbda_backward_prologue(const void* q_raw, const int64_t* q_strides,
                            int64_t length, int64_t head_dim, int32_t dtype,
                            const int32_t* offsets, int32_t num_offsets,
                            const int32_t* seg_key, void* stream);
+
+/*
+ * Forward over source tables (see "Source tables" above).  Writes out and
+ * lse like sbda_forward / sbda_forward_prologue.
+ */
+int sbda_forward_paths(const void* q, const int64_t* q_strides,
+                       const void* k, const int64_t* k_strides,
+                       const void* v, const int64_t* v_strides,
+                       void* out, const int64_t* out_strides,
+                       float* lse,
+                       const float* q_weight, const float* k_weight,
+                       const float* rope_cos, const float* rope_sin, float eps,
+                       int64_t batch, int64_t heads, int64_t kv_heads,
+                       int64_t length, int64_t head_dim, int32_t dtype,
+                       const int64_t* path_indices, const uint8_t* path_valid,
+                       int32_t num_sources, const int32_t* seg_key, void* stream);
+
+/* Workspace bytes sbda_backward_paths needs (prologue: 1 if the prologue
+ * pointers will be given, else 0; < 0: error). */
+int64_t sbda_backward_paths_workspace(int64_t batch, int64_t heads, int64_t kv_heads,
+                                      int64_t length, int64_t head_dim, int32_t dtype,
+                                      int32_t num_sources, int32_t prologue);
+
+/*
+ * Backward of sbda_forward_paths: gradients of q, k, v (raw q/k with the
+ * prologue) and, with the prologue, of the two norm weights.  The workspace
+ * (256-byte aligned) holds a per-(row, slot) weight table and an inverse
+ * index built by a stable sort, so every gradient row is written once, in a
+ * fixed order: deterministic, no atomics.  dq_weight/dk_weight may be NULL
+ * without the prologue.
+ */
+int sbda_backward_paths(const void* q, const int64_t* q_strides,
+                        const void* k, const int64_t* k_strides,
+                        const void* v, const int64_t* v_strides,
+                        const void* dout, const int64_t* dout_strides,
+                        const float* lse,
+                        const float* q_weight, const float* k_weight,
+                        const float* rope_cos, const float* rope_sin, float eps,
+                        void* dq, const int64_t* dq_strides,
+                        void* dk, const int64_t* dk_strides,
+                        void* dv, const int64_t* dv_strides,
+                        float* dq_weight, float* dk_weight,
+                        void* workspace, int64_t workspace_bytes,
+                        int64_t batch, int64_t heads, int64_t kv_heads,
+                        int64_t length, int64_t head_dim, int32_t dtype,
+                        const int64_t* path_indices, const uint8_t* path_valid,
+                        int32_t num_sources, const int32_t* seg_key, void* stream);
 
 /*
  * RoPE tables: cos/sin[t, i] = cos/sin(fl32(t * inv_freq[i])) for t < length,

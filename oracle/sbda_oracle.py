@@ -13,13 +13,17 @@ What is restated, and from where (paths relative to the reference checkout):
   matmul route ``use_sdpa=True`` and the elementwise route)
 * ``attention_lse``           -- the log-normaliser of the softmax in
   ``left_v2.py:385-392`` (the fused path saves it per row)
-* ``brute_force_attention``   -- the paper's formula (``paper_en.md:44-81``)
-  as scalar loops, for tiny fp64 cases
+* ``brute_force_attention`` / ``brute_force_sources`` -- the paper's formula
+  (``paper_en.md:44-81``) as scalar loops, for tiny fp64 cases
 * ``key_gather_backward``     -- the key-centric closed form of the backward
   that ``BiAttn/sbda_triton.py:507-671`` specifies (dQ from weights, dK/dV
   gathered per key, no scatter)
 * ``prologue``                -- ``left_v2.py:237-239`` (head-RMSNorm of q
   and k, then half-split RoPE)
+* ``masked_source_valid`` / ``gather_attention_masked`` -- the eager route's
+  ``valid_mask`` / ``seam_reset`` masking (``left_v2.py:329-378``)
+* ``table_source_valid`` / ``gather_attention_tables`` -- the same route over
+  caller-supplied ``path_indices`` / ``path_valid`` (``left_v2.py:313-378``)
 * ``valid_cell_count`` / ``unique_cell_count`` -- the cell statistics of
   ``BinaryDiffusionAttention/run_graph_coverage.py:47-89``
 
@@ -255,6 +259,33 @@ def brute_force_attention(q: Tensor, k: Tensor, v: Tensor,
     return out, lse
 
 
+def brute_force_sources(q: Tensor, k: Tensor, v: Tensor,
+                        sources: Sequence[Sequence[Sequence[int]]]) -> Tensor:
+    """Scalar-loop fp64 softmax attention where query ``i`` of batch ``b`` reads
+    the positions ``sources[b][i]`` (repeats count repeatedly; an empty list
+    gives a zero row).  Tiny inputs only."""
+    b_, h_, t_, d_ = q.shape
+    group = h_ // k.shape[1]
+    qd, kd, vd = (x.double().tolist() for x in (q, k, v))
+    out = torch.zeros(b_, h_, t_, d_, dtype=torch.float64)
+    scale = 1.0 / math.sqrt(d_)
+    for b in range(b_):
+        for h in range(h_):
+            hk = h // group
+            for i in range(t_):
+                srcs = list(sources[b][i])
+                if not srcs:
+                    continue
+                sc = [scale * sum(qd[b][h][i][e] * kd[b][hk][j][e] for e in range(d_))
+                      for j in srcs]
+                m = max(sc)
+                ex = [math.exp(x - m) for x in sc]
+                z = sum(ex)
+                for e in range(d_):
+                    out[b, h, i, e] = sum(w * vd[b][hk][j][e] for w, j in zip(ex, srcs)) / z
+    return out
+
+
 def key_gather_backward(q: Tensor, k: Tensor, v: Tensor, dout: Tensor,
                         offsets: Sequence[int]) -> tuple[Tensor, Tensor, Tensor]:
     """Gradients in the key-centric (gather) form, each row written once.
@@ -326,6 +357,47 @@ def masked_source_valid(length: int, offsets: Sequence[int], valid_mask: Tensor 
     return idx, valid
 
 
+def table_source_valid(path_indices: Tensor, path_valid: Tensor | None,
+                       valid_mask: Tensor | None, seam_reset: Tensor | None) -> Tensor:
+    """``source_valid [B, T, S]`` for caller-supplied tables (``left_v2.py:349-378``):
+    ``path_valid`` (all set when absent), causality ``idx <= i`` (``:355-357``),
+    then the same ``valid_mask`` / ``seam_reset`` rules as the offset route,
+    including slot 0 forced valid for padded query rows (``:371``)."""
+    b, t, s = path_indices.shape
+    valid = torch.ones(b, t, s, dtype=torch.bool)
+    if path_valid is not None:
+        valid &= path_valid
+    positions = torch.arange(t)
+    valid &= path_indices <= positions[None, :, None]
+    if valid_mask is not None:
+        valid &= valid_mask.unsqueeze(-1).expand(-1, -1, s).gather(1, path_indices)
+        if seam_reset is not None:
+            seg = seam_reset.to(torch.int64).cumsum(dim=1)
+            valid &= seg.unsqueeze(-1).expand(-1, -1, s).gather(1, path_indices) == seg[:, :, None]
+        valid[:, :, 0] |= ~valid_mask
+    elif seam_reset is not None:
+        seg = seam_reset.to(torch.int64).cumsum(dim=1)
+        valid &= seg.unsqueeze(-1).expand(-1, -1, s).gather(1, path_indices) == seg[:, :, None]
+    return valid
+
+
+def _table_attention(q: Tensor, k: Tensor, v: Tensor, idx: Tensor, valid: Tensor) -> Tensor:
+    """``left_v2.py:333-396`` with per-batch tables ``idx``/``valid [B, T, S]``:
+    gather, scaled scores, ``finfo.min`` fill, softmax, zero fill, weighted sum."""
+    b, h, t, d = q.shape
+    k = _expand_kv(k, h)
+    v = _expand_kv(v, h)
+    s = idx.shape[-1]
+    src = idx[:, None, :, :, None].expand(b, h, t, s, d)
+    kg = k.unsqueeze(3).expand(b, h, t, s, d).gather(2, src)
+    vg = v.unsqueeze(3).expand(b, h, t, s, d).gather(2, src)
+    invalid = ~valid[:, None]
+    scores = torch.matmul(q.unsqueeze(-2), kg.transpose(-1, -2)).squeeze(-2) * (d ** -0.5)
+    scores = scores.masked_fill(invalid, torch.finfo(scores.dtype).min)
+    weights = scores.softmax(dim=-1).masked_fill(invalid, 0.0)
+    return torch.matmul(weights.unsqueeze(-2), vg).squeeze(-2)
+
+
 def gather_attention_masked(q: Tensor, k: Tensor, v: Tensor, offsets: Sequence[int],
                             valid_mask: Tensor | None = None,
                             seam_reset: Tensor | None = None) -> Tensor:
@@ -334,16 +406,16 @@ def gather_attention_masked(q: Tensor, k: Tensor, v: Tensor, offsets: Sequence[i
     ``valid_mask`` multiply)."""
     if valid_mask is None and seam_reset is None:
         return gather_attention(q, k, v, offsets)
-    b, h, t, d = q.shape
-    k = _expand_kv(k, h)
-    v = _expand_kv(v, h)
+    b, _, t, _ = q.shape
     idx, valid = masked_source_valid(t, offsets, valid_mask, seam_reset)
-    s = idx.shape[1]
-    src = idx[None, None, :, :, None].expand(b, h, t, s, d)
-    kg = k.unsqueeze(3).expand(b, h, t, s, d).gather(2, src)
-    vg = v.unsqueeze(3).expand(b, h, t, s, d).gather(2, src)
-    invalid = ~valid[:, None]
-    scores = torch.matmul(q.unsqueeze(-2), kg.transpose(-1, -2)).squeeze(-2) * (d ** -0.5)
-    scores = scores.masked_fill(invalid, torch.finfo(scores.dtype).min)
-    weights = scores.softmax(dim=-1).masked_fill(invalid, 0.0)
-    return torch.matmul(weights.unsqueeze(-2), vg).squeeze(-2)
+    return _table_attention(q, k, v, idx.unsqueeze(0).expand(b, -1, -1), valid)
+
+
+def gather_attention_tables(q: Tensor, k: Tensor, v: Tensor, path_indices: Tensor,
+                            path_valid: Tensor | None = None,
+                            valid_mask: Tensor | None = None,
+                            seam_reset: Tensor | None = None) -> Tensor:
+    """Eager attention over caller-supplied source tables (``left_v2.py:313-405``
+    with ``path_indices [B, T, S]`` int64 in ``[0, T)`` and ``path_valid``)."""
+    valid = table_source_valid(path_indices, path_valid, valid_mask, seam_reset)
+    return _table_attention(q, k, v, path_indices, valid)

@@ -14,12 +14,15 @@ from .sbda import (
     fused_sbda_block_full,
     fused_sbda_gqa_key_backward,
     fused_sbda_key_backward,
+    fused_sbda_paths,
     fused_sbda_prologue,
     host_offsets,
     rope_inverse_frequencies,
     rope_tables,
     sbda_backward,
+    sbda_backward_paths,
     sbda_forward,
+    sbda_forward_paths,
     segment_keys,
 )
 from .topology import PATH_TOPOLOGIES, sbda_stage, topology_offsets
@@ -31,7 +34,8 @@ __all__ = [
     "BiAttnBlock", "BiAttnConfig", "BiAttnLM", "BinaryPathAttention", "LIBRARY_PATH",
     "PATH_TOPOLOGIES", "SBDAAttention", "SBDALibraryError", "SBDAttention", "fused_sbda",
     "fused_sbda_block", "fused_sbda_block_full", "fused_sbda_gqa_key_backward",
-    "fused_sbda_key_backward", "fused_sbda_prologue", "host_offsets",
-    "rope_inverse_frequencies", "rope_tables", "sbda_backward", "sbda_forward",
+    "fused_sbda_key_backward", "fused_sbda_paths", "fused_sbda_prologue", "host_offsets",
+    "rope_inverse_frequencies", "rope_tables", "sbda_backward", "sbda_backward_paths",
+    "sbda_forward", "sbda_forward_paths",
     "sbda_stage", "segment_keys", "topology_offsets",
 ]

@@ -11,7 +11,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("libsbda_amd.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 OK, ERR_VALUE, ERR_DTYPE, ERR_RUNTIME = 0, 1, 2, 3
 _ERRORS = {ERR_VALUE: ValueError, ERR_DTYPE: TypeError, ERR_RUNTIME: RuntimeError}
@@ -44,6 +44,18 @@ SIGNATURES = {
                                               _strides, _fptr, _fptr, _fptr, _p, _p, _f32,
                                               _p, _strides, _p, _strides, _p, _strides,
                                               _fptr, _fptr, _p, _i64, *_SHAPE, _SEG, _p]),
+    "sbda_forward_paths": (ctypes.c_int, [_p, _strides, _p, _strides, _p, _strides, _p, _strides,
+                                          _fptr, _fptr, _fptr, _p, _p, _f32,
+                                          _i64, _i64, _i64, _i64, _i64, _i32, _p, _p, _i32,
+                                          _SEG, _p]),
+    "sbda_backward_paths_workspace": (ctypes.c_int64, [_i64, _i64, _i64, _i64, _i64, _i32, _i32,
+                                                       _i32]),
+    "sbda_backward_paths": (ctypes.c_int, [_p, _strides, _p, _strides, _p, _strides, _p, _strides,
+                                           _fptr, _fptr, _fptr, _p, _p, _f32,
+                                           _p, _strides, _p, _strides, _p, _strides,
+                                           _fptr, _fptr, _p, _i64,
+                                           _i64, _i64, _i64, _i64, _i64, _i32, _p, _p, _i32,
+                                           _SEG, _p]),
     "sbda_rope_table": (ctypes.c_int, [_p, _p, ctypes.POINTER(ctypes.c_float), _i64, _i64, _p]),
 }
 

@@ -9,14 +9,14 @@ parameter names (``q``, ``k``, ``v``, ``q_norm.weight``, ``k_norm.weight``,
 The fused route is the only route: projections run in PyTorch, then
 head-RMSNorm + RoPE + SBDA attention run as one HIP op
 (:func:`sbda.fused_sbda_prologue`), then the output projection and the
-``valid_mask`` multiply (``left_v2.py:295-305``).  Masks the reference sends
-to its eager gather path -- a ``valid_mask`` with interior holes and
-``seam_reset`` (``left_v2.py:329-378``) -- run in the same HIP op through a
-per-position segment key (:func:`sbda.segment_keys`).  What remains eager-only
-in the reference -- caller-supplied ``path_indices``/``path_valid``, routes
-with other than two or four offsets, ``use_fused``/``use_sdpa`` off, a CPU
-tensor -- raises ``NotImplementedError`` here rather than silently taking a
-slower path.
+``valid_mask`` multiply (``left_v2.py:295-305``).  What the reference sends
+to its eager gather path also runs in HIP here: a ``valid_mask`` with
+interior holes and ``seam_reset`` (``left_v2.py:329-378``) through a
+per-position segment key (:func:`sbda.segment_keys`), caller-supplied
+``path_indices``/``path_valid`` through the source-table kernels
+(:func:`sbda.fused_sbda_paths`).  What is left -- offset routes with other
+than two or four offsets, ``use_fused``/``use_sdpa`` off, a CPU tensor --
+raises ``NotImplementedError`` rather than silently taking a slower path.
 """
 
 from __future__ import annotations
@@ -95,14 +95,23 @@ class BinaryPathAttention(nn.Module):
                 raise ValueError("path_indices must have shape [batch, sequence, source_count]")
             if path_indices.dtype != torch.long:
                 raise ValueError("path_indices must use torch.long")
+            if path_indices.device != x.device:
+                raise ValueError("path_indices must be on the same device as x")
+            if path_valid is not None and (path_valid.shape != path_indices.shape
+                                           or path_valid.dtype != torch.bool
+                                           or path_valid.device != x.device):
+                raise ValueError("path_valid must match path_indices as a bool tensor")
+            if path_indices.numel() and (int(path_indices.min()) < 0
+                                         or int(path_indices.max()) >= length):
+                raise ValueError("path_indices contains an out-of-range source")
 
     def forward(self, x: Tensor, valid_mask: Tensor | None = None,
                 seam_reset: Tensor | None = None, path_indices: Tensor | None = None,
                 path_valid: Tensor | None = None) -> Tensor:
         self._check_inputs(x, valid_mask, seam_reset, path_indices, path_valid)
         batch, length, dim = x.shape
-        # A right-padded prefix mask is safe for the fused route
-        # (left_v2.py:252-262): causal sources never read the padding.
+        # A right-padded prefix mask needs no per-source check (left_v2.py:252-262):
+        # causal sources of a valid row are valid.
         prefix_mask = (valid_mask is None or valid_mask.shape[1] < 2
                        or bool(torch.all(~valid_mask[:, 1:] | valid_mask[:, :-1])))
         reasons = []
@@ -110,15 +119,14 @@ class BinaryPathAttention(nn.Module):
             reasons.append("a CPU tensor")
         if not (self.use_fused and self.use_sdpa):
             reasons.append("use_fused/use_sdpa disabled")
-        if path_indices is not None or path_valid is not None:
-            reasons.append("caller-supplied path tables")
-        if len(self.offsets) not in (2, 4):
+        if path_indices is None and path_valid is not None:
+            reasons.append("path_valid without path_indices")
+        if path_indices is None and len(self.offsets) not in (2, 4):
             reasons.append(f"{len(self.offsets)} offsets")
         if reasons:
             raise NotImplementedError(
                 "SBDA-AMD runs only the reference's fused route; this call needs the eager "
                 "gather path because of " + ", ".join(reasons))
-        # A prefix mask needs no key: causal sources of a valid row are valid.
         seg_key = None if prefix_mask and seam_reset is None else segment_keys(
             valid_mask, seam_reset)
         q = self.q(x).view(batch, length, self.heads, self.head_dim)
@@ -127,7 +135,8 @@ class BinaryPathAttention(nn.Module):
         attended = fused_sbda_prologue(
             q.permute(0, 2, 1, 3), k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3),
             self._fused_offsets, self.q_norm.weight, self.k_norm.weight,
-            theta=self.rope_theta, eps=self.q_norm.eps, seg_key=seg_key)
+            theta=self.rope_theta, eps=self.q_norm.eps, seg_key=seg_key,
+            path_indices=path_indices, path_valid=path_valid)
         out = self.out(attended.transpose(1, 2).reshape(batch, length, dim))
         if valid_mask is not None:
             out = out * valid_mask[:, :, None].to(dtype=out.dtype)

@@ -19,6 +19,10 @@ hipError_t walk_forward(const Params& p, int dtype, bool pro, hipStream_t st);
 hipError_t walk_backward(const Params& p, int dtype, bool pro, hipStream_t st);
 void walk_partials(const Params& p, int dtype, int64_t* parts_q, int64_t* parts_k,
                    int64_t* tab_floats);
+int64_t paths_workspace(const Params& p, int esz, bool pro, int64_t* parts_q, int64_t* parts_k);
+hipError_t paths_forward(const Params& p, int dtype, bool pro, hipStream_t st);
+hipError_t paths_backward(Params p, int dtype, bool pro, void* ws, int64_t parts_q, hipStream_t st,
+                          float** dwq_part, float** dwk_part);
 
 namespace {
 
@@ -37,10 +41,9 @@ int fail(int code, const char* fmt, ...) {
 
 int esize(int dtype) { return dtype == kFP32 ? 4 : 2; }
 
-// Shapes, dtype and offsets shared by every entry point.
-int check_problem(int64_t batch, int64_t heads, int64_t kv_heads, int64_t length,
-                  int64_t head_dim, int32_t dtype, const int32_t* offsets,
-                  int32_t num_offsets, Params& p) {
+// Shapes and dtype shared by every entry point.
+int check_shape(int64_t batch, int64_t heads, int64_t kv_heads, int64_t length, int64_t head_dim,
+                int32_t dtype, Params& p) {
   if (dtype != kBF16 && dtype != kFP16 && dtype != kFP32)
     return fail(SBDA_ERR_DTYPE, "unsupported SBDA dtype code %d (bf16, fp16 or fp32)", (int)dtype);
   if (batch <= 0 || heads <= 0 || kv_heads <= 0 || length <= 0 || head_dim <= 0)
@@ -58,21 +61,49 @@ int check_problem(int64_t batch, int64_t heads, int64_t kv_heads, int64_t length
                 "head_dim %lld unsupported: head_dim * element size must be a multiple of 16 bytes "
                 "and at most 512 bytes",
                 (long long)head_dim);
-  if (offsets == nullptr || num_offsets < 1 || num_offsets > kMaxSlots)
-    return fail(SBDA_ERR_VALUE, "SBDA supports 1 to %d sources, got %d", kMaxSlots, (int)num_offsets);
   std::memset(&p, 0, sizeof(p));
-  for (int s = 0; s < num_offsets; ++s) {
-    if (offsets[s] < 0) return fail(SBDA_ERR_VALUE, "SBDA offsets must be >= 0 (slot %d is %d)", s, offsets[s]);
-    p.off[s] = offsets[s];
-  }
   p.B = (int)batch;
   p.H = (int)heads;
   p.Hkv = (int)kv_heads;
   p.group = (int)(heads / kv_heads);
   p.T = (int)length;
   p.D = (int)head_dim;
-  p.S = num_offsets;
   p.scale = (float)(1.0 / __builtin_sqrt((double)head_dim));
+  return SBDA_OK;
+}
+
+// Shapes, dtype and offsets of the offset-mode entry points.
+int check_problem(int64_t batch, int64_t heads, int64_t kv_heads, int64_t length,
+                  int64_t head_dim, int32_t dtype, const int32_t* offsets,
+                  int32_t num_offsets, Params& p) {
+  int rc = check_shape(batch, heads, kv_heads, length, head_dim, dtype, p);
+  if (rc) return rc;
+  if (offsets == nullptr || num_offsets < 1 || num_offsets > kMaxSlots)
+    return fail(SBDA_ERR_VALUE, "SBDA supports 1 to %d sources, got %d", kMaxSlots, (int)num_offsets);
+  for (int s = 0; s < num_offsets; ++s) {
+    if (offsets[s] < 0) return fail(SBDA_ERR_VALUE, "SBDA offsets must be >= 0 (slot %d is %d)", s, offsets[s]);
+    p.off[s] = offsets[s];
+  }
+  p.S = num_offsets;
+  return SBDA_OK;
+}
+
+// Shapes, dtype and source tables of the table-mode entry points.
+int check_paths(int64_t batch, int64_t heads, int64_t kv_heads, int64_t length, int64_t head_dim,
+                int32_t dtype, const int64_t* pidx, const uint8_t* pvalid, int32_t num_sources,
+                const int32_t* seg, Params& p) {
+  int rc = check_shape(batch, heads, kv_heads, length, head_dim, dtype, p);
+  if (rc) return rc;
+  if (num_sources < 1) return fail(SBDA_ERR_VALUE, "source tables need at least one source");
+  if (batch * length * num_sources >= (int64_t(1) << 31) - 1)
+    return fail(SBDA_ERR_VALUE, "source tables exceed 2^31 entries");
+  if (pidx == nullptr) return fail(SBDA_ERR_VALUE, "path_indices: null pointer");
+  if (reinterpret_cast<uintptr_t>(pidx) % 8)
+    return fail(SBDA_ERR_VALUE, "path_indices must be 8-byte aligned");
+  p.pidx = pidx;
+  p.pvalid = pvalid;
+  p.PS = num_sources;
+  p.seg = seg;
   return SBDA_OK;
 }
 
@@ -204,6 +235,87 @@ int backward_impl(bool pro, const void* q, const int64_t* qs, const void* k, con
   return hip_status(e, "sbda backward launch");
 }
 
+int set_prologue(Params& p, const float* wq, const float* wk, const float* rc, const float* rs,
+                 float eps, bool* pro) {
+  *pro = wq != nullptr || wk != nullptr || rc != nullptr || rs != nullptr;
+  if (!*pro) return SBDA_OK;
+  if (!wq || !wk || !rc || !rs)
+    return fail(SBDA_ERR_VALUE, "prologue: give all of q_weight, k_weight, rope_cos, rope_sin or none");
+  p.wq = wq;
+  p.wk = wk;
+  p.rope_cos = rc;
+  p.rope_sin = rs;
+  p.eps = eps;
+  return SBDA_OK;
+}
+
+int paths_forward_impl(const void* q, const int64_t* qs, const void* k, const int64_t* ks,
+                       const void* v, const int64_t* vs, void* out, const int64_t* os, float* lse,
+                       const float* wq, const float* wk, const float* rc, const float* rs, float eps,
+                       int64_t batch, int64_t heads, int64_t kv_heads, int64_t length,
+                       int64_t head_dim, int32_t dtype, const int64_t* pidx, const uint8_t* pvalid,
+                       int32_t ns, const int32_t* seg, void* stream) {
+  g_error.clear();
+  Params p;
+  int rc_ = check_paths(batch, heads, kv_heads, length, head_dim, dtype, pidx, pvalid, ns, seg, p);
+  if (rc_) return rc_;
+  const int esz = esize(dtype);
+  if ((rc_ = check_view("q", q, qs, esz, false, &p.q))) return rc_;
+  if ((rc_ = check_view("k", k, ks, esz, false, &p.k))) return rc_;
+  if ((rc_ = check_view("v", v, vs, esz, false, &p.v))) return rc_;
+  if ((rc_ = check_mut("out", out, os, esz, &p.o))) return rc_;
+  if (lse == nullptr) return fail(SBDA_ERR_VALUE, "lse: null pointer");
+  p.lse = lse;
+  bool pro = false;
+  if ((rc_ = set_prologue(p, wq, wk, rc, rs, eps, &pro))) return rc_;
+  return hip_status(paths_forward(p, dtype, pro, reinterpret_cast<hipStream_t>(stream)),
+                    "sbda table-mode forward launch");
+}
+
+int paths_backward_impl(const void* q, const int64_t* qs, const void* k, const int64_t* ks,
+                        const void* v, const int64_t* vs, const void* dout, const int64_t* dos,
+                        const float* lse, const float* wq, const float* wk, const float* rc,
+                        const float* rs, float eps, void* dq, const int64_t* dqs, void* dk,
+                        const int64_t* dks, void* dv, const int64_t* dvs, float* dwq, float* dwk,
+                        void* ws, int64_t ws_bytes, int64_t batch, int64_t heads, int64_t kv_heads,
+                        int64_t length, int64_t head_dim, int32_t dtype, const int64_t* pidx,
+                        const uint8_t* pvalid, int32_t ns, const int32_t* seg, void* stream) {
+  g_error.clear();
+  Params p;
+  int rc_ = check_paths(batch, heads, kv_heads, length, head_dim, dtype, pidx, pvalid, ns, seg, p);
+  if (rc_) return rc_;
+  const int esz = esize(dtype);
+  if ((rc_ = check_view("q", q, qs, esz, false, &p.q))) return rc_;
+  if ((rc_ = check_view("k", k, ks, esz, false, &p.k))) return rc_;
+  if ((rc_ = check_view("v", v, vs, esz, false, &p.v))) return rc_;
+  if ((rc_ = check_view("grad_out", dout, dos, esz, false, &p.dout))) return rc_;
+  if ((rc_ = check_mut("dq", dq, dqs, esz, &p.dq))) return rc_;
+  if ((rc_ = check_mut("dk", dk, dks, esz, &p.dk))) return rc_;
+  if ((rc_ = check_mut("dv", dv, dvs, esz, &p.dv))) return rc_;
+  if (lse == nullptr) return fail(SBDA_ERR_VALUE, "lse: null pointer");
+  p.lse = const_cast<float*>(lse);
+  bool pro = false;
+  if ((rc_ = set_prologue(p, wq, wk, rc, rs, eps, &pro))) return rc_;
+  if (pro && (!dwq || !dwk)) return fail(SBDA_ERR_VALUE, "prologue: null weight-gradient output");
+  int64_t pq = 0, pk = 0;
+  const int64_t need = paths_workspace(p, esz, pro, &pq, &pk);
+  if (need < 0) return fail(SBDA_ERR_RUNTIME, "table-mode backward: cannot size the sort storage");
+  if (ws == nullptr || ws_bytes < need)
+    return fail(SBDA_ERR_VALUE, "table-mode backward: workspace of %lld bytes needed, %lld given",
+                (long long)need, (long long)ws_bytes);
+  if (reinterpret_cast<uintptr_t>(ws) % 256)
+    return fail(SBDA_ERR_VALUE, "workspace must be 256-byte aligned");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  float* dwq_part = nullptr;
+  float* dwk_part = nullptr;
+  hipError_t e = paths_backward(p, dtype, pro, ws, pq, st, &dwq_part, &dwk_part);
+  if (e == hipSuccess && pro) {
+    e = launch_reduce_partials(dwq_part, pq, p.D, dwq, st);
+    if (e == hipSuccess) e = launch_reduce_partials(dwk_part, pk, p.D, dwk, st);
+  }
+  return hip_status(e, "sbda table-mode backward launch");
+}
+
 }  // namespace
 }  // namespace sbda
 
@@ -211,7 +323,7 @@ using namespace sbda;
 
 extern "C" {
 
-int sbda_abi_version(void) { return 4; }
+int sbda_abi_version(void) { return 5; }
 
 const char* sbda_last_error(void) { return g_error.c_str(); }
 
@@ -272,6 +384,49 @@ int sbda_backward_prologue(const void* q, const int64_t* qs, const void* k, cons
   return backward_impl(true, q, qs, k, ks, v, vs, dout, dos, lse, wq, wk, rc, rs, eps, dq, dqs, dk,
                        dks, dv, dvs, dwq, dwk, ws, ws_bytes, batch, heads, kv_heads, length, head_dim,
                        dtype, offsets, n, seg_key, stream);
+}
+
+int sbda_forward_paths(const void* q, const int64_t* qs, const void* k, const int64_t* ks,
+                       const void* v, const int64_t* vs, void* out, const int64_t* os, float* lse,
+                       const float* wq, const float* wk, const float* rc, const float* rs, float eps,
+                       int64_t batch, int64_t heads, int64_t kv_heads, int64_t length,
+                       int64_t head_dim, int32_t dtype, const int64_t* path_indices,
+                       const uint8_t* path_valid, int32_t num_sources, const int32_t* seg_key,
+                       void* stream) {
+  return paths_forward_impl(q, qs, k, ks, v, vs, out, os, lse, wq, wk, rc, rs, eps, batch, heads,
+                            kv_heads, length, head_dim, dtype, path_indices, path_valid,
+                            num_sources, seg_key, stream);
+}
+
+int64_t sbda_backward_paths_workspace(int64_t batch, int64_t heads, int64_t kv_heads,
+                                      int64_t length, int64_t head_dim, int32_t dtype,
+                                      int32_t num_sources, int32_t prologue) {
+  g_error.clear();
+  Params p;
+  int rc = check_shape(batch, heads, kv_heads, length, head_dim, dtype, p);
+  if (rc) return -rc;
+  if (num_sources < 1 || batch * length * num_sources >= (int64_t(1) << 31) - 1)
+    return -fail(SBDA_ERR_VALUE, "source tables need 1 to 2^31 entries");
+  p.PS = num_sources;
+  int64_t pq = 0, pk = 0;
+  const int64_t need = paths_workspace(p, esize(dtype), prologue != 0, &pq, &pk);
+  if (need < 0) return -fail(SBDA_ERR_RUNTIME, "table-mode backward: cannot size the sort storage");
+  return need;
+}
+
+int sbda_backward_paths(const void* q, const int64_t* qs, const void* k, const int64_t* ks,
+                        const void* v, const int64_t* vs, const void* dout, const int64_t* dos,
+                        const float* lse, const float* wq, const float* wk, const float* rc,
+                        const float* rs, float eps, void* dq, const int64_t* dqs, void* dk,
+                        const int64_t* dks, void* dv, const int64_t* dvs, float* dwq, float* dwk,
+                        void* ws, int64_t ws_bytes, int64_t batch, int64_t heads,
+                        int64_t kv_heads, int64_t length, int64_t head_dim, int32_t dtype,
+                        const int64_t* path_indices, const uint8_t* path_valid,
+                        int32_t num_sources, const int32_t* seg_key, void* stream) {
+  return paths_backward_impl(q, qs, k, ks, v, vs, dout, dos, lse, wq, wk, rc, rs, eps, dq, dqs, dk,
+                             dks, dv, dvs, dwq, dwk, ws, ws_bytes, batch, heads, kv_heads, length,
+                             head_dim, dtype, path_indices, path_valid, num_sources, seg_key,
+                             stream);
 }
 
 int sbda_rope_table(float* rope_cos, float* rope_sin, const float* inv_freq, int64_t length,

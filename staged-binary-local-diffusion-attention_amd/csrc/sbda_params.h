@@ -38,6 +38,15 @@ struct Params {
   // Optional segment keys [B, T] (row stride T): a source j of query i counts
   // only if key[i] >= 0 and key[j] == key[i].  nullptr = no masking.
   const int32_t* seg;
+  // Source-table mode (sbda_paths.hip): PS sources per query read from
+  // pidx [B, T, PS] int64 (contiguous), gated by pvalid [B, T, PS] bytes
+  // (nullptr = all set).  inv_start [B*T + 1] / inv_entry (i * PS + s, sorted)
+  // list, per key position b*T + j, the (query, slot) pairs that read it.
+  const int64_t* pidx;
+  const uint8_t* pvalid;
+  int PS;
+  const uint32_t* inv_start;
+  const uint32_t* inv_entry;
 };
 
 enum DType : int { kBF16 = 0, kFP16 = 1, kFP32 = 2 };

@@ -9,8 +9,10 @@ backend, see below), parameter names and weight initialisation
 Only what the SBDA route uses is here: ``attention_backend`` must be
 ``"sbda"`` (the default in this mirror), the feed-forward is the dense SwiGLU,
 token IO is a plain (tied) embedding.  The reference's other backends, the
-DeepSeekMoE feed-forward, factorized token IO and ``path_active`` raise
-``ValueError``/``NotImplementedError``.
+DeepSeekMoE feed-forward and factorized token IO raise ``ValueError``.
+Per-layer source tables (``path_indices [B, layers, T, S]``) and the
+per-row layer switch ``path_active [B, layers]`` follow
+``BiAttn/model.py:397-466``.
 """
 
 from __future__ import annotations
@@ -175,14 +177,49 @@ class BiAttnLM(nn.Module):
         if valid_mask is not None and (valid_mask.shape != input_ids.shape
                                        or valid_mask.dtype != torch.bool):
             raise ValueError("valid_mask must be bool with input_ids shape")
-        if path_active is not None:
-            raise NotImplementedError("path_active is not supported by the SBDA-AMD backbone")
+        if seam_reset is not None and (seam_reset.shape != input_ids.shape
+                                       or seam_reset.dtype != torch.bool):
+            raise ValueError("seam_reset must be bool with input_ids shape")
+        if path_indices is not None and (
+                path_indices.ndim != 4 or path_indices.shape[0] != input_ids.shape[0]
+                or path_indices.shape[2] != input_ids.shape[1]
+                or path_indices.dtype != torch.long):
+            raise ValueError("path_indices must have shape [batch, layers, sequence, source_count]")
+        if path_valid is not None and (path_indices is None
+                                       or path_valid.shape != path_indices.shape
+                                       or path_valid.dtype != torch.bool):
+            raise ValueError("path_valid must match path_indices as a bool tensor")
+        if path_active is not None and (path_indices is None or path_active.ndim != 2
+                                        or path_active.shape != path_indices.shape[:2]
+                                        or path_active.dtype != torch.bool
+                                        or path_active.device != input_ids.device):
+            raise ValueError("path_active must have shape [batch, layers] and match path_indices")
+        if path_indices is not None and path_indices.shape[1] != len(self.layers):
+            raise ValueError("path_indices layer count must match the model")
         # An all-true mask is dropped once here (model.py:439-440).
         if valid_mask is not None and bool(valid_mask.all()):
             valid_mask = None
         x = self.drop(self.embedding(input_ids))
-        for layer in self.layers:
-            x = layer(x, valid_mask, seam_reset, path_indices, path_valid)
+        for index, layer in enumerate(self.layers):
+            if path_active is None:
+                x = layer(x, valid_mask, seam_reset, path_indices, path_valid)
+                continue
+            # Rows whose layer is inactive pass through unchanged (model.py:446-466).
+            active = path_active[:, index]
+            if not bool(active.any()):
+                continue
+            if bool(active.all()):
+                x = layer(x, valid_mask, seam_reset, path_indices, path_valid)
+                continue
+            rows = active.nonzero(as_tuple=False).flatten()
+
+            def pick(t):
+                return None if t is None else t.index_select(0, rows)
+
+            updated = layer(x.index_select(0, rows), pick(valid_mask), pick(seam_reset),
+                            pick(path_indices), pick(path_valid))
+            x = x.clone()
+            x.index_copy_(0, rows, updated)
         return self.norm(x)
 
     def forward(self, input_ids: Tensor, valid_mask: Optional[Tensor] = None,

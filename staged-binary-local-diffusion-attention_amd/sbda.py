@@ -20,7 +20,9 @@ reference's other backward variants of the same maths
 Every op takes an optional ``seg_key`` (int32 ``[B, T]``, see
 :func:`segment_keys`): the source masking of the reference's eager route
 (``valid_mask`` holes and ``seam_reset`` segments, ``left_v2.py:329-378``)
-as one key per position.
+as one key per position.  ``fused_sbda_paths`` (and ``fused_sbda_prologue``
+with ``path_indices=``) take caller-supplied source tables instead of
+offsets (``left_v2.py:212-231,313-378``).
 
 Errors follow the reference's classes (``sbda_triton.py:1295-1302``):
 ``RuntimeError`` for a non-GPU tensor, ``ValueError`` for shapes / source
@@ -241,6 +243,132 @@ fused_sbda_block = fused_sbda_key_backward
 fused_sbda_block_full = fused_sbda_key_backward
 
 
+# ------------------------------------------------------ source-table ops
+
+def _paths_check(q, path_indices, path_valid):
+    b, _, t, _ = q.shape
+    if (path_indices.ndim != 3 or tuple(path_indices.shape[:2]) != (b, t)
+            or path_indices.shape[2] < 1):
+        raise ValueError("path_indices must have shape [batch, sequence, source_count]")
+    if path_indices.dtype != torch.long:
+        raise ValueError("path_indices must use torch.long")
+    if path_indices.device != q.device:
+        raise ValueError("path_indices must be on the same device as x")
+    pidx = path_indices.contiguous()
+    pval = None
+    if path_valid is not None:
+        if (path_valid.shape != path_indices.shape or path_valid.dtype != torch.bool
+                or path_valid.device != q.device):
+            raise ValueError("path_valid must match path_indices as a bool tensor")
+        pval = path_valid.contiguous()
+    return pidx, pval
+
+
+def _prologue_ptrs(pro):
+    if pro is None:
+        return (ctypes.c_void_p(0),) * 4 + (0.0,)
+    wq, wk, cos, sin, eps = pro
+    return _ptr(wq), _ptr(wk), _ptr(cos), _ptr(sin), float(eps)
+
+
+def _paths_shape(q, k, pidx):
+    b, h, t, d = q.shape
+    return (b, h, k.shape[1], t, d, _DTYPES[q.dtype])
+
+
+def sbda_forward_paths(q, k, v, path_indices, path_valid=None, seg_key=None, *, prologue=None):
+    """Table-mode forward without autograd: ``(out [B,H,T,D], lse [B,H,T])``.
+
+    ``prologue``: ``(q_weight32, k_weight32, cos, sin, eps)`` to fuse the
+    head-RMSNorm + RoPE of raw q/k, or ``None``."""
+    _validate(q, k, v, (0, 0), gqa=True)
+    pidx, pval = _paths_check(q, path_indices, path_valid)
+    lib = _lib.load()
+    q, k, v = (_kernel_view(x) for x in (q, k, v))
+    out = torch.empty_like(q)
+    b, h, t, _ = q.shape
+    lse = _lse_storage(b, h, t, q.device)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.sbda_forward_paths(
+            _ptr(q), _lib.strides(q), _ptr(k), _lib.strides(k), _ptr(v), _lib.strides(v),
+            _ptr(out), _lib.strides(out), _ptr(lse), *_prologue_ptrs(prologue),
+            *_paths_shape(q, k, pidx), _ptr(pidx), _ptr(pval), pidx.shape[2],
+            _seg_arg(seg_key, q), _stream(q)))
+    return out, lse
+
+
+def sbda_backward_paths(q, k, v, grad_out, lse, path_indices, path_valid=None, seg_key=None,
+                        *, prologue=None):
+    """Table-mode backward: ``(dq, dk, dv, dq_weight, dk_weight)``, the last
+    two fp32 ``[D]`` with the prologue and ``None`` without."""
+    _validate(q, k, v, (0, 0), gqa=True)
+    pidx, pval = _paths_check(q, path_indices, path_valid)
+    lib = _lib.load()
+    q, k, v, grad_out = (_kernel_view(x) for x in (q, k, v, grad_out))
+    if grad_out.shape != q.shape or grad_out.dtype != q.dtype:
+        raise ValueError("grad_out must match q's shape and dtype")
+    if lse.shape != q.shape[:3] or lse.dtype != torch.float32:
+        raise ValueError("lse must be the fp32 [B,H,T] log-normalisers of the forward")
+    lse = _lse_buffer(lse)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    d = q.shape[-1]
+    dwq = dwk = None
+    if prologue is not None:
+        dwq = torch.empty(d, dtype=torch.float32, device=q.device)
+        dwk = torch.empty_like(dwq)
+    shape = _paths_shape(q, k, pidx)
+    need = lib.sbda_backward_paths_workspace(*shape, pidx.shape[2], int(prologue is not None))
+    if need < 0:
+        _lib.check(-need)
+    ws = torch.empty(int(need) + 256, dtype=torch.uint8, device=q.device)
+    ws_view = ws[(-ws.data_ptr()) % 256:]
+    with torch.cuda.device(q.device):
+        _lib.check(lib.sbda_backward_paths(
+            _ptr(q), _lib.strides(q), _ptr(k), _lib.strides(k), _ptr(v), _lib.strides(v),
+            _ptr(grad_out), _lib.strides(grad_out), _ptr(lse), *_prologue_ptrs(prologue),
+            _ptr(dq), _lib.strides(dq), _ptr(dk), _lib.strides(dk), _ptr(dv), _lib.strides(dv),
+            _ptr(dwq), _ptr(dwk), _ptr(ws_view), ws_view.numel(),
+            *shape, _ptr(pidx), _ptr(pval), pidx.shape[2], _seg_arg(seg_key, q), _stream(q)))
+    return dq, dk, dv, dwq, dwk
+
+
+class _FusedSBDAPaths(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, q_weight, k_weight, path_indices, path_valid, seg_key, theta, eps):
+        pro = None
+        if q_weight is not None:
+            d = q.shape[-1]
+            wq, wk = _weight32(q_weight, d, q.device), _weight32(k_weight, d, q.device)
+            cos, sin = rope_tables(q.shape[2], d, theta, q.device)
+            pro = (wq, wk, cos, sin, float(eps))
+            ctx.wdtypes = (q_weight.dtype, k_weight.dtype)
+        out, lse = sbda_forward_paths(q, k, v, path_indices, path_valid, seg_key, prologue=pro)
+        ctx.save_for_backward(_kernel_view(q), _kernel_view(k), _kernel_view(v), lse)
+        ctx.tables = (path_indices, path_valid, seg_key)
+        ctx.pro = pro
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        q, k, v, lse = ctx.saved_tensors
+        g = grad_out if grad_out.dtype == q.dtype else grad_out.to(q.dtype)
+        dq, dk, dv, dwq, dwk = sbda_backward_paths(q, k, v, g, lse, *ctx.tables, prologue=ctx.pro)
+        if ctx.pro is not None:
+            dwq, dwk = dwq.to(ctx.wdtypes[0]), dwk.to(ctx.wdtypes[1])
+        return dq, dk, dv, dwq, dwk, None, None, None, None, None
+
+
+def fused_sbda_paths(q, k, v, path_indices, path_valid=None, *, seg_key=None):
+    """SBDA attention over caller-supplied source tables, ``[B,H,T,D]`` in and out.
+
+    ``path_indices``: int64 ``[B, T, S]`` source positions, ``path_valid``:
+    bool ``[B, T, S]`` or ``None``; a source counts when valid, ``j <= i`` and
+    (with ``seg_key``) in the query's segment -- the eager route of
+    ``BiAttn/left_v2.py:313-378``.  ``k``/``v`` may have fewer heads (GQA)."""
+    return _FusedSBDAPaths.apply(q, k, v, None, None, path_indices, path_valid, seg_key,
+                                 0.0, 0.0)
+
+
 # ------------------------------------------------------- fused prologue op
 
 _ROPE_CACHE: "OrderedDict[tuple, tuple[torch.Tensor, torch.Tensor]]" = OrderedDict()
@@ -338,14 +466,20 @@ class _FusedSBDAPrologue(torch.autograd.Function):
 
 
 def fused_sbda_prologue(q_raw, k_raw, v, offsets, q_weight, k_weight, *,
-                        theta: float, eps: float = 1e-6, seg_key=None):
+                        theta: float, eps: float = 1e-6, seg_key=None,
+                        path_indices=None, path_valid=None):
     """Head-RMSNorm(q, k) -> RoPE -> SBDA attention in one fused op.
 
     ``q_raw``: ``[B, H, T, D]`` projections before normalisation; ``k_raw``,
     ``v``: ``[B, Hkv, T, D]``; ``q_weight``/``k_weight``: ``[D]`` norm
     weights.  Equals ``fused_sbda_key_backward(rope(norm(q)), rope(norm(k)),
     v, offsets)`` with the reference's prologue (``BiAttn/left_v2.py:237-239``).
+    With ``path_indices`` (and optionally ``path_valid``) the sources come from
+    those tables and ``offsets`` is ignored (see :func:`fused_sbda_paths`).
     """
+    if path_indices is not None:
+        return _FusedSBDAPaths.apply(q_raw, k_raw, v, q_weight, k_weight, path_indices,
+                                     path_valid, seg_key, float(theta), float(eps))
     return _FusedSBDAPrologue.apply(q_raw, k_raw, v, q_weight, k_weight, offsets,
                                     float(theta), float(eps), seg_key)
 
@@ -353,6 +487,7 @@ def fused_sbda_prologue(q_raw, k_raw, v, offsets, q_weight, k_weight, *,
 __all__ = [
     "fused_sbda", "fused_sbda_block", "fused_sbda_block_full",
     "fused_sbda_key_backward", "fused_sbda_gqa_key_backward",
-    "fused_sbda_prologue", "host_offsets", "rope_inverse_frequencies", "rope_tables",
-    "sbda_backward", "sbda_forward", "segment_keys",
+    "fused_sbda_paths", "fused_sbda_prologue", "host_offsets", "rope_inverse_frequencies", "rope_tables",
+    "sbda_backward", "sbda_backward_paths", "sbda_forward", "sbda_forward_paths",
+    "segment_keys",
 ]

@@ -308,7 +308,8 @@ def test_tile_edges_and_offset_patterns(t, offs):
 
 # ------------------------------------------------------------ module level
 
-def _oracle_module_forward(m, x, valid_mask=None, seam_reset=None):
+def _oracle_module_forward(m, x, valid_mask=None, seam_reset=None, path_indices=None,
+                           path_valid=None):
     """The reference module's forward (left_v2.py:234-306 fused route, or the
     eager masked gather of :313-405 for holes / seams), restated with the
     oracle's prologue and gather attention."""
@@ -319,7 +320,10 @@ def _oracle_module_forward(m, x, valid_mask=None, seam_reset=None):
     q, k = ref.prologue(q, k, m.q_norm.weight, m.k_norm.weight, m.rope_theta)
     qh, kh, vh = (x_.permute(0, 2, 1, 3) for x_ in (q, k, v))
     prefix = valid_mask is None or bool(torch.all(~valid_mask[:, 1:] | valid_mask[:, :-1]))
-    if prefix and seam_reset is None:
+    if path_indices is not None:
+        att = ref.gather_attention_tables(qh, kh, vh, path_indices, path_valid, valid_mask,
+                                          seam_reset)
+    elif prefix and seam_reset is None:
         att = ref.gather_attention(qh, kh, vh, m.offsets)
     else:
         att = ref.gather_attention_masked(qh, kh, vh, m.offsets, valid_mask, seam_reset)
@@ -365,12 +369,12 @@ def test_sbdattention_module_matches_oracle_module(layer, kv_heads):
 def test_sbdattention_module_rejects_eager_only_inputs():
     m = sbda_amd.SBDAttention(64, 4, 3).to(DEV)
     x = torch.randn(1, 8, 64, device=DEV)
-    paths = torch.zeros(1, 8, 4, dtype=torch.long, device=DEV)
-    with pytest.raises(NotImplementedError, match="path tables"):
-        m(x, None, None, paths)
     off = sbda_amd.SBDAttention(64, 4, 3, use_fused=False).to(DEV)
     with pytest.raises(NotImplementedError, match="use_fused"):
         off(x)
+    bad = torch.full((1, 8, 2), 8, dtype=torch.long, device=DEV)
+    with pytest.raises(ValueError, match="out-of-range"):
+        m(x, None, None, bad)
 
 
 # ------------------------------------------------------------ masks
@@ -513,6 +517,172 @@ def test_backbone_forward_backward_matches_oracle_composition():
         return model.lm_head(model.norm(x))
 
     want = oracle_forward(mc, ids, valid)
+    want.float().square().mean().backward()
+    torch.testing.assert_close(out.detach().cpu(), want.detach(), rtol=1e-4, atol=1e-4)
+    for (name, p), (_, pc) in zip(md.named_parameters(), mc.named_parameters()):
+        scale = pc.grad.abs().max().item() + 1e-8
+        err = (p.grad.cpu() - pc.grad).abs().max().item()
+        assert err / scale < 1e-3, f"{name}: {err} vs scale {scale}"
+
+
+# ------------------------------------------------------------ source tables
+
+def _tables(b, t, s, seed):
+    """Mostly near-causal source tables with some future entries, a
+    duplicate, and random path_valid flags."""
+    g = torch.Generator().manual_seed(seed)
+    anywhere = torch.randint(0, t, (b, t, s), generator=g)
+    near = (torch.arange(t)[None, :, None]
+            - torch.randint(0, 40, (b, t, s), generator=g)).clamp_min(0)
+    idx = torch.where(torch.rand(b, t, s, generator=g) < 0.8, near, anywhere)
+    if s > 2:
+        idx[:, 5, 1:3] = 2
+    valid = torch.rand(b, t, s, generator=g) > 0.15
+    return idx, valid
+
+
+def _table_run(fn, q, k, v, g):
+    qd, kd, vd = (_dev(x).requires_grad_() for x in (q, k, v))
+    out = fn(qd, kd, vd)
+    out.backward(_dev(g))
+    torch.cuda.synchronize()
+    return [x.detach().float().cpu() for x in (out, qd.grad, kd.grad, vd.grad)]
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, FP32_TOL), (torch.bfloat16, LOW_TOL)])
+@pytest.mark.parametrize("s,hkv,d", [(1, None, 64), (3, None, 64), (5, 2, 64), (8, 4, 40),
+                                     (4, None, 128)])
+@pytest.mark.parametrize("masked", [False, True])
+def test_table_op_matches_oracle(dtype, tol, s, hkv, d, masked):
+    b, t, h = 2, 300, 8
+    q, k, v, g = _inputs(b, t, h, d, dtype, seed=s * 13 + d + int(masked), hkv=hkv)
+    idx, valid = _tables(b, t, s, seed=s + d)
+    vm, sr = _masks(b, t, seed=s) if masked else (None, None)
+    keep = torch.ones(b, t, dtype=torch.bool) if vm is None else vm
+    g = g * keep[:, :, None, None].to(dtype)
+    key = sbda_amd.segment_keys(vm.to(DEV), sr.to(DEV)) if masked else None
+    pidx, pval = idx.to(DEV), valid.to(DEV)
+    got = _table_run(lambda a, bb, c: sbda_amd.fused_sbda_paths(a, bb, c, pidx, pval, seg_key=key),
+                     q, k, v, g)
+    rq, rk, rv = (x.float().permute(0, 2, 1, 3).requires_grad_() for x in (q, k, v))
+    want = ref.gather_attention_tables(rq, rk, rv, idx, valid, vm, sr)
+    want.backward(g.float().permute(0, 2, 1, 3))
+    rows = keep[:, None, :, None].expand_as(got[0])
+    assert torch.all(got[0][~rows] == 0)
+    torch.testing.assert_close(got[0][rows], want.detach()[rows], **tol)
+    for name, a, r in zip(("dq", "dk", "dv"), got[1:], (rq.grad, rk.grad, rv.grad)):
+        torch.testing.assert_close(a, r, **tol, msg=lambda m: f"S={s} {name}: {m}")
+
+
+def test_tables_from_offsets_match_the_offset_op():
+    b, t, h, d = 1, 1000, 8, 64
+    q, k, v, g = _inputs(b, t, h, d, torch.bfloat16, seed=123)
+    for offs in ((0, 2), (0, 1, 2, 16), (0, 1, 2, 512)):
+        idx, ok = ref.path_tables(t, offs)
+        pidx = idx.unsqueeze(0).to(DEV).contiguous()
+        pval = ok.unsqueeze(0).to(DEV).contiguous()
+        off = torch.tensor(offs, dtype=torch.int32, device=DEV)
+        a = _table_run(lambda x, y, z: sbda_amd.fused_sbda_paths(x, y, z, pidx, pval), q, k, v, g)
+        w = _table_run(lambda x, y, z: sbda_amd.fused_sbda_key_backward(x, y, z, off), q, k, v, g)
+        _close(a, w, LOW_TOL, f"tables vs offsets {offs}")
+
+
+def test_table_backward_is_bitwise_deterministic():
+    b, t, h, d, s = 2, 700, 8, 64, 6
+    q, k, v, g = _inputs(b, t, h, d, torch.bfloat16, seed=7)
+    idx, valid = _tables(b, t, s, seed=8)
+    pidx, pval = idx.to(DEV), valid.to(DEV)
+    fn = lambda x, y, z: sbda_amd.fused_sbda_paths(x, y, z, pidx, pval)  # noqa: E731
+    first = _table_run(fn, q, k, v, g)
+    second = _table_run(fn, q, k, v, g)
+    for a, bb in zip(first, second):
+        assert torch.equal(a, bb)
+
+
+def test_table_module_reference_known_answers():
+    # tests/test_model.py:19-42 on the module: a slot pointing at a future
+    # position is masked, and all-invalid tables give zero output and gradient.
+    torch.manual_seed(42)
+    attn = sbda_amd.SBDAttention(32, 4, 3, kv_heads=2).to(DEV)
+    x = torch.randn(1, 8, 32, device=DEV, requires_grad=True)
+    paths = torch.arange(8, device=DEV).view(1, 8, 1).expand(1, 8, 2).clone()
+    paths[:, :, 1] = 7
+    y = attn(x, path_indices=paths)
+    changed = x.detach().clone()
+    changed[:, 4:] += 10
+    torch.testing.assert_close(y[:, :4], attn(changed, path_indices=paths)[:, :4])
+    y[:, :4].square().sum().backward()
+    assert x.grad[:, 4:].abs().max().item() == 0
+    attn2 = sbda_amd.SBDAttention(32, 4, 3).to(DEV)
+    x2 = torch.randn(1, 8, 32, device=DEV, requires_grad=True)
+    zeros = torch.zeros(1, 8, 2, dtype=torch.long, device=DEV)
+    y2 = attn2(x2, path_indices=zeros, path_valid=torch.zeros_like(zeros, dtype=torch.bool))
+    assert y2.abs().max().item() == 0
+    y2.sum().backward()
+    assert x2.grad.abs().max().item() == 0
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_sbdattention_module_with_tables_matches_oracle(masked):
+    torch.manual_seed(80)
+    dim, heads, t, s = 256, 4, 300, 5
+    m = sbda_amd.SBDAttention(dim, heads, 6, kv_heads=2, rope_theta=10000.0, total_layers=12)
+    with torch.no_grad():
+        m.q_norm.weight.mul_(1 + 0.1 * torch.randn(m.head_dim))
+        m.k_norm.weight.mul_(1 + 0.1 * torch.randn(m.head_dim))
+    x = torch.randn(2, t, dim)
+    idx, valid = _tables(2, t, s, seed=81)
+    vm, sr = _masks(2, t, seed=82) if masked else (None, None)
+    g = torch.randn(2, t, dim)
+    md = m.to(DEV)
+    xd = x.to(DEV).requires_grad_()
+    out = md(xd, None if vm is None else vm.to(DEV), None if sr is None else sr.to(DEV),
+             idx.to(DEV), valid.to(DEV))
+    out.backward(g.to(DEV))
+    torch.cuda.synchronize()
+    mc = sbda_amd.SBDAttention(dim, heads, 6, kv_heads=2, rope_theta=10000.0, total_layers=12)
+    mc.load_state_dict({k_: v_.cpu() for k_, v_ in md.state_dict().items()})
+    xc = x.clone().requires_grad_()
+    want = _oracle_module_forward(mc, xc, vm, sr, idx, valid)
+    want.backward(g)
+    tol = dict(rtol=1e-4, atol=1e-4)
+    torch.testing.assert_close(out.detach().cpu(), want.detach(), **tol)
+    torch.testing.assert_close(xd.grad.cpu(), xc.grad, **tol)
+    for (name, p), (_, pc) in zip(md.named_parameters(), mc.named_parameters()):
+        scale = pc.grad.abs().max().item() + 1e-6
+        err = (p.grad.cpu() - pc.grad).abs().max().item()
+        assert err / scale < 1e-4, f"{name}: {err} vs scale {scale}"
+
+
+def test_backbone_with_tables_and_path_active_matches_oracle():
+    # BiAttn/model.py:397-466: per-layer tables; path_active skips a layer for
+    # some rows (those rows pass through unchanged).
+    torch.manual_seed(61)
+    layers, t, s = 3, 200, 4
+    cfg = sbda_amd.BiAttnConfig(vocab_size=64, dim=128, layers=layers, heads=2,
+                                rope_theta=10000.0, ff_hidden=256)
+    m = sbda_amd.BiAttnLM(cfg)
+    ids = torch.randint(0, 64, (3, t))
+    idx = torch.stack([_tables(3, t, s, seed=90 + l)[0] for l in range(layers)], dim=1)
+    valid = torch.stack([_tables(3, t, s, seed=90 + l)[1] for l in range(layers)], dim=1)
+    active = torch.tensor([[True, True, True], [True, False, True], [False, False, True]])
+    md = m.to(DEV)
+    out = md(ids.to(DEV), None, None, idx.to(DEV), valid.to(DEV), active.to(DEV))
+    out.float().square().mean().backward()
+    torch.cuda.synchronize()
+    mc = sbda_amd.BiAttnLM(cfg)
+    mc.load_state_dict({k_: v_.cpu() for k_, v_ in md.state_dict().items()})
+
+    def oracle_forward(model):
+        x = model.embedding(ids)
+        for li, blk in enumerate(model.layers):
+            y = x + _oracle_module_forward(blk.attn, blk.norm1(x), None, None,
+                                           idx[:, li], valid[:, li])
+            y = y + blk.ff(blk.norm2(y))
+            x = torch.where(active[:, li, None, None], y, x)
+        return model.lm_head(model.norm(x))
+
+    want = oracle_forward(mc)
     want.float().square().mean().backward()
     torch.testing.assert_close(out.detach().cpu(), want.detach(), rtol=1e-4, atol=1e-4)
     for (name, p), (_, pc) in zip(md.named_parameters(), mc.named_parameters()):

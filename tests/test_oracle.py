@@ -342,3 +342,83 @@ def test_masked_gradcheck_fp64():
     q, k, v = (_rand(1, 2, t, 3, seed=s).requires_grad_() for s in (66, 67, 68))
     assert torch.autograd.gradcheck(
         lambda a, b, c: ref.gather_attention_masked(a, b, c, (0, 1, 2, 4), valid, seam), (q, k, v))
+
+
+# ------------------------------------------------------------ source tables
+
+def _random_tables(b, t, s, seed):
+    g = torch.Generator().manual_seed(seed)
+    idx = torch.randint(0, t, (b, t, s), generator=g)
+    idx[:, :, 0] = torch.arange(t)                     # self in slot 0
+    idx[:, 3, 1] = idx[:, 3, 2] = 1                    # a duplicate source
+    valid = torch.rand(b, t, s, generator=g) > 0.2
+    return idx, valid
+
+
+def test_tables_match_brute_force_with_duplicates_and_future_entries():
+    b, h, t, d, s = 2, 2, 9, 4, 4
+    q, k, v = (_rand(b, h, t, d, seed=70 + i) for i in range(3))
+    idx, valid = _random_tables(b, t, s, seed=71)
+    got = ref.gather_attention_tables(q, k, v, idx, valid)
+    sources = [[[int(idx[bb, i, ss]) for ss in range(s)
+                 if bool(valid[bb, i, ss]) and int(idx[bb, i, ss]) <= i]
+                for i in range(t)] for bb in range(b)]
+    torch.testing.assert_close(got, ref.brute_force_sources(q, k, v, sources),
+                               rtol=1e-12, atol=1e-12)
+
+
+def test_tables_from_offsets_equal_the_offset_route():
+    b, h, t, d = 2, 4, 37, 8
+    q, k, v = (_rand(b, h, t, d, seed=80 + i) for i in range(3))
+    valid_mask = torch.rand(b, t, generator=torch.Generator().manual_seed(81)) > 0.2
+    seam = torch.zeros(b, t, dtype=torch.bool)
+    seam[1, 20] = True
+    for offs in ((0, 1), (0, 1, 2, 8), (0, 1, 2, 64)):
+        idx, ok = ref.path_tables(t, offs)
+        tab = idx.unsqueeze(0).expand(b, -1, -1).contiguous()
+        okb = ok.unsqueeze(0).expand(b, -1, -1).contiguous()
+        torch.testing.assert_close(ref.gather_attention_tables(q, k, v, tab, okb),
+                                   ref.gather_attention(q, k, v, offs), rtol=0, atol=0)
+        torch.testing.assert_close(
+            ref.gather_attention_tables(q, k, v, tab, okb, valid_mask, seam),
+            ref.gather_attention_masked(q, k, v, offs, valid_mask, seam), rtol=0, atol=0)
+
+
+def test_tables_reference_known_answers():
+    # tests/test_model.py:19-42: slot 1 points at position 7 for every row, so
+    # rows before 7 see only themselves; all-invalid tables give zero rows.
+    t, d = 8, 4
+    q, k, v = (_rand(1, 2, t, d, seed=90 + i) for i in range(3))
+    paths = torch.arange(t).view(1, t, 1).expand(1, t, 2).clone()
+    paths[:, :, 1] = 7
+    out = ref.gather_attention_tables(q, k, v, paths)
+    torch.testing.assert_close(out[:, :, :7], v[:, :, :7], rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(out[:, :, 7], v[:, :, 7], rtol=1e-12, atol=1e-12)
+    qg = q.clone().requires_grad_()
+    none = ref.gather_attention_tables(qg, k, v, paths, torch.zeros_like(paths, dtype=torch.bool))
+    assert none.abs().max().item() == 0
+    none.sum().backward()
+    assert qg.grad.abs().max().item() == 0
+
+
+def test_duplicate_source_is_a_log2_score_bias():
+    # Listing j twice weighs it like one entry with score + log 2.
+    b, h, t, d = 1, 1, 6, 4
+    q, k, v = (_rand(b, h, t, d, seed=95 + i) for i in range(3))
+    i = 5
+    idx = torch.tensor([[[r, max(r - 1, 0), max(r - 1, 0)] for r in range(t)]])
+    ok = idx <= torch.arange(t)[None, :, None]
+    got = ref.gather_attention_tables(q, k, v, idx, ok)[0, 0, i]
+    s_self = (q[0, 0, i] @ k[0, 0, i]) / math.sqrt(d)
+    s_prev = (q[0, 0, i] @ k[0, 0, i - 1]) / math.sqrt(d) + math.log(2)
+    w = torch.softmax(torch.stack([s_self, s_prev]), 0)
+    torch.testing.assert_close(got, w[0] * v[0, 0, i] + w[1] * v[0, 0, i - 1],
+                               rtol=1e-12, atol=1e-12)
+
+
+def test_tables_gradcheck_fp64():
+    b, h, hkv, t, d, s = 1, 2, 1, 6, 3, 3
+    q, k, v = (_rand(b, hh, t, d, seed=99 + i).requires_grad_() for i, hh in enumerate((h, hkv, hkv)))
+    idx, valid = _random_tables(b, t, s, seed=98)
+    assert torch.autograd.gradcheck(
+        lambda a, bb, c: ref.gather_attention_tables(a, bb, c, idx, valid), (q, k, v))

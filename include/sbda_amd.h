@@ -204,6 +204,45 @@ int sbda_backward_paths(const void* q, const int64_t* q_strides,
                         int32_t num_sources, const int32_t* seg_key, void* stream);
 
 /*
+ * Block kernels next to the attention op (BiAttn/model.py:18-59,321-335).
+ * They have no C counterpart in the reference (there they are eager PyTorch
+ * ops: F.rms_norm, the residual `x + ...`, F.silu(gate(x)) * up(x)); they
+ * fuse those ops so each activation crosses HBM once.  Buffers are
+ * contiguous row-major [rows, width], 16-byte aligned, width * element size a
+ * multiple of 16 bytes.
+ *
+ * sbda_rmsnorm_forward: y = (s * rsqrt(mean(s^2) + eps)) * weight with
+ * s = x, or s = x + residual (rounded to dtype, written to sum_out) when
+ * residual is given.  weight is fp32 [dim]; rstd (optional, fp32 [rows])
+ * receives the per-row rsqrt for the backward.  dim * element size <= 8 KiB.
+ */
+int sbda_rmsnorm_forward(const void* x, const void* residual, void* sum_out, void* y,
+                         const float* weight, float* rstd, int64_t rows, int64_t dim,
+                         int32_t dtype, float eps, void* stream);
+
+/* Workspace bytes of sbda_rmsnorm_backward (< 0: error). */
+int64_t sbda_rmsnorm_backward_workspace(int64_t rows, int64_t dim, int32_t dtype);
+
+/*
+ * Backward of sbda_rmsnorm_forward: dx = d(y)/d(s) applied to dy, plus dsum
+ * (the gradient reaching s from its other uses, optional); dx is then the
+ * gradient of x and of residual.  dweight (fp32 [dim]) is overwritten with
+ * the weight gradient, summed in a fixed order through `workspace`.
+ */
+int sbda_rmsnorm_backward(const void* dy, const void* x, const float* weight, const float* rstd,
+                          const void* dsum, void* dx, float* dweight, void* workspace,
+                          int64_t workspace_bytes, int64_t rows, int64_t dim, int32_t dtype,
+                          void* stream);
+
+/* SwiGLU activation: out[r, c] = silu(gate_up[r, c]) * gate_up[r, hidden + c]. */
+int sbda_swiglu_forward(const void* gate_up, void* out, int64_t rows, int64_t hidden,
+                        int32_t dtype, void* stream);
+
+/* Backward of sbda_swiglu_forward into dgate_up ([rows, 2 * hidden]). */
+int sbda_swiglu_backward(const void* dout, const void* gate_up, void* dgate_up, int64_t rows,
+                         int64_t hidden, int32_t dtype, void* stream);
+
+/*
  * RoPE tables: cos/sin[t, i] = cos/sin(fl32(t * inv_freq[i])) for t < length,
  * i < head_dim/2, as fp32 [length, head_dim/2].  inv_freq is a host fp32
  * array of head_dim/2 values (head_dim <= 512).

@@ -25,6 +25,7 @@ from .sbda import (
     sbda_forward_paths,
     segment_keys,
 )
+from .block import fused_add_rms_norm, fused_rms_norm, fused_swiglu
 from .topology import PATH_TOPOLOGIES, sbda_stage, topology_offsets
 from .attention import BinaryPathAttention, SBDAAttention, SBDAttention
 from .model import BiAttnBlock, BiAttnConfig, BiAttnLM
@@ -32,7 +33,8 @@ from ._lib import LIBRARY_PATH, SBDALibraryError
 
 __all__ = [
     "BiAttnBlock", "BiAttnConfig", "BiAttnLM", "BinaryPathAttention", "LIBRARY_PATH",
-    "PATH_TOPOLOGIES", "SBDAAttention", "SBDALibraryError", "SBDAttention", "fused_sbda",
+    "PATH_TOPOLOGIES", "SBDAAttention", "SBDALibraryError", "SBDAttention",
+    "fused_add_rms_norm", "fused_rms_norm", "fused_swiglu", "fused_sbda",
     "fused_sbda_block", "fused_sbda_block_full", "fused_sbda_gqa_key_backward",
     "fused_sbda_key_backward", "fused_sbda_paths", "fused_sbda_prologue", "host_offsets",
     "rope_inverse_frequencies", "rope_tables", "sbda_backward", "sbda_backward_paths",

@@ -23,6 +23,7 @@ from __future__ import annotations
 
 import torch
 from torch import Tensor, nn
+from torch.nn import functional as F
 
 from .sbda import fused_sbda_prologue, segment_keys
 from .topology import PATH_TOPOLOGIES, topology_offsets
@@ -129,9 +130,13 @@ class BinaryPathAttention(nn.Module):
                 "gather path because of " + ", ".join(reasons))
         seg_key = None if prefix_mask and seam_reset is None else segment_keys(
             valid_mask, seam_reset)
-        q = self.q(x).view(batch, length, self.heads, self.head_dim)
-        k = self.k(x).view(batch, length, self.kv_heads, self.head_dim)
-        v = self.v(x).view(batch, length, self.kv_heads, self.head_dim)
+        # One GEMM for q, k and v; the kernels read the three column blocks of
+        # its output in place (strided views, no copies).
+        kvd = self.kv_heads * self.head_dim
+        qkv = F.linear(x, torch.cat((self.q.weight, self.k.weight, self.v.weight), dim=0))
+        q = qkv[..., :dim].view(batch, length, self.heads, self.head_dim)
+        k = qkv[..., dim:dim + kvd].view(batch, length, self.kv_heads, self.head_dim)
+        v = qkv[..., dim + kvd:].view(batch, length, self.kv_heads, self.head_dim)
         attended = fused_sbda_prologue(
             q.permute(0, 2, 1, 3), k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3),
             self._fused_offsets, self.q_norm.weight, self.k_norm.weight,

@@ -23,6 +23,18 @@ int64_t paths_workspace(const Params& p, int esz, bool pro, int64_t* parts_q, in
 hipError_t paths_forward(const Params& p, int dtype, bool pro, hipStream_t st);
 hipError_t paths_backward(Params p, int dtype, bool pro, void* ws, int64_t parts_q, hipStream_t st,
                           float** dwq_part, float** dwk_part);
+int64_t rmsnorm_bwd_blocks(int64_t rows);
+int rmsnorm_max_dim(int esz);
+hipError_t rmsnorm_forward(const void* x, const void* r, void* s_out, void* y, const float* w,
+                           float* rstd, int64_t rows, int dim, int dtype, float eps,
+                           hipStream_t st);
+hipError_t rmsnorm_backward(const void* dy, const void* s, const float* w, const float* rstd,
+                            const void* ds_in, void* dx, float* part, int64_t rows, int dim,
+                            int dtype, hipStream_t st);
+hipError_t swiglu_forward(const void* gu, void* h, int64_t rows, int hidden, int dtype,
+                          hipStream_t st);
+hipError_t swiglu_backward(const void* dh, const void* gu, void* dgu, int64_t rows, int hidden,
+                           int dtype, hipStream_t st);
 
 namespace {
 
@@ -316,6 +328,23 @@ int paths_backward_impl(const void* q, const int64_t* qs, const void* k, const i
   return hip_status(e, "sbda table-mode backward launch");
 }
 
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+// Rows x width problems of the block kernels: contiguous rows, 16-byte
+// aligned buffers, width a whole number of 16-byte chunks.
+int check_rows(int64_t rows, int64_t width, int32_t dtype, int64_t max_width) {
+  if (dtype != kBF16 && dtype != kFP16 && dtype != kFP32)
+    return fail(SBDA_ERR_DTYPE, "unsupported dtype code %d (bf16, fp16 or fp32)", (int)dtype);
+  if (rows <= 0 || width <= 0) return fail(SBDA_ERR_VALUE, "rows and width must be positive");
+  if ((width * esize(dtype)) % 16)
+    return fail(SBDA_ERR_VALUE, "width %lld: rows must be a multiple of 16 bytes", (long long)width);
+  if (width > max_width)
+    return fail(SBDA_ERR_VALUE, "width %lld exceeds the supported %lld", (long long)width,
+                (long long)max_width);
+  if (rows >= (int64_t(1) << 40)) return fail(SBDA_ERR_VALUE, "too many rows");
+  return SBDA_OK;
+}
+
 }  // namespace
 }  // namespace sbda
 
@@ -323,7 +352,7 @@ using namespace sbda;
 
 extern "C" {
 
-int sbda_abi_version(void) { return 5; }
+int sbda_abi_version(void) { return 6; }
 
 const char* sbda_last_error(void) { return g_error.c_str(); }
 
@@ -427,6 +456,77 @@ int sbda_backward_paths(const void* q, const int64_t* qs, const void* k, const i
                              dks, dv, dvs, dwq, dwk, ws, ws_bytes, batch, heads, kv_heads, length,
                              head_dim, dtype, path_indices, path_valid, num_sources, seg_key,
                              stream);
+}
+
+int sbda_rmsnorm_forward(const void* x, const void* residual, void* sum_out, void* y,
+                         const float* weight, float* rstd, int64_t rows, int64_t dim,
+                         int32_t dtype, float eps, void* stream) {
+  g_error.clear();
+  int rc = check_rows(rows, dim, dtype, rmsnorm_max_dim(esize(dtype)));
+  if (rc) return rc;
+  if (!x || !y || !weight) return fail(SBDA_ERR_VALUE, "rmsnorm: null x, y or weight");
+  if (residual && !sum_out) return fail(SBDA_ERR_VALUE, "rmsnorm: residual given without sum_out");
+  if (!aligned16(x) || !aligned16(y) || (residual && (!aligned16(residual) || !aligned16(sum_out))))
+    return fail(SBDA_ERR_VALUE, "rmsnorm: buffers must be 16-byte aligned");
+  return hip_status(rmsnorm_forward(x, residual, sum_out, y, weight, rstd, rows, (int)dim, dtype,
+                                    eps, reinterpret_cast<hipStream_t>(stream)),
+                    "sbda rmsnorm forward launch");
+}
+
+int64_t sbda_rmsnorm_backward_workspace(int64_t rows, int64_t dim, int32_t dtype) {
+  g_error.clear();
+  int rc = check_rows(rows, dim, dtype, rmsnorm_max_dim(esize(dtype)));
+  if (rc) return -rc;
+  return rmsnorm_bwd_blocks(rows) * 4 * dim * (int64_t)sizeof(float);
+}
+
+int sbda_rmsnorm_backward(const void* dy, const void* x, const float* weight, const float* rstd,
+                          const void* dsum, void* dx, float* dweight, void* workspace,
+                          int64_t workspace_bytes, int64_t rows, int64_t dim, int32_t dtype,
+                          void* stream) {
+  g_error.clear();
+  int rc = check_rows(rows, dim, dtype, rmsnorm_max_dim(esize(dtype)));
+  if (rc) return rc;
+  if (!dy || !x || !weight || !rstd || !dx || !dweight)
+    return fail(SBDA_ERR_VALUE, "rmsnorm backward: null pointer");
+  if (!aligned16(dy) || !aligned16(x) || !aligned16(dx) || (dsum && !aligned16(dsum)))
+    return fail(SBDA_ERR_VALUE, "rmsnorm backward: buffers must be 16-byte aligned");
+  const int64_t parts = rmsnorm_bwd_blocks(rows) * 4;
+  const int64_t need = parts * dim * (int64_t)sizeof(float);
+  if (!workspace || workspace_bytes < need)
+    return fail(SBDA_ERR_VALUE, "rmsnorm backward: workspace of %lld bytes needed, %lld given",
+                (long long)need, (long long)workspace_bytes);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  float* part = static_cast<float*>(workspace);
+  hipError_t e = rmsnorm_backward(dy, x, weight, rstd, dsum, dx, part, rows, (int)dim, dtype, st);
+  if (e == hipSuccess) e = launch_reduce_partials(part, parts, (int)dim, dweight, st);
+  return hip_status(e, "sbda rmsnorm backward launch");
+}
+
+int sbda_swiglu_forward(const void* gate_up, void* out, int64_t rows, int64_t hidden,
+                        int32_t dtype, void* stream) {
+  g_error.clear();
+  int rc = check_rows(rows, hidden, dtype, int64_t(1) << 24);
+  if (rc) return rc;
+  if (!gate_up || !out) return fail(SBDA_ERR_VALUE, "swiglu: null pointer");
+  if (!aligned16(gate_up) || !aligned16(out))
+    return fail(SBDA_ERR_VALUE, "swiglu: buffers must be 16-byte aligned");
+  return hip_status(swiglu_forward(gate_up, out, rows, (int)hidden, dtype,
+                                   reinterpret_cast<hipStream_t>(stream)),
+                    "sbda swiglu forward launch");
+}
+
+int sbda_swiglu_backward(const void* dout, const void* gate_up, void* dgate_up, int64_t rows,
+                         int64_t hidden, int32_t dtype, void* stream) {
+  g_error.clear();
+  int rc = check_rows(rows, hidden, dtype, int64_t(1) << 24);
+  if (rc) return rc;
+  if (!dout || !gate_up || !dgate_up) return fail(SBDA_ERR_VALUE, "swiglu backward: null pointer");
+  if (!aligned16(dout) || !aligned16(gate_up) || !aligned16(dgate_up))
+    return fail(SBDA_ERR_VALUE, "swiglu backward: buffers must be 16-byte aligned");
+  return hip_status(swiglu_backward(dout, gate_up, dgate_up, rows, (int)hidden, dtype,
+                                    reinterpret_cast<hipStream_t>(stream)),
+                    "sbda swiglu backward launch");
 }
 
 int sbda_rope_table(float* rope_cos, float* rope_sin, const float* inv_freq, int64_t length,

@@ -26,10 +26,13 @@ from torch import Tensor, nn
 from torch.nn import functional as F
 
 from .attention import SBDAttention
+from .block import fused_add_rms_norm, fused_rms_norm, fused_swiglu
 
 
 class RMSNorm(nn.Module):
-    """``BiAttn/model.py:18-29``."""
+    """``BiAttn/model.py:18-29``.  Device tensors run the HIP kernel
+    (:func:`block.fused_rms_norm`); CPU tensors run ``F.rms_norm`` as the
+    reference module does."""
 
     def __init__(self, dim: int, eps: float = 1e-6) -> None:
         super().__init__()
@@ -38,7 +41,13 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(dim))
 
     def forward(self, x: Tensor) -> Tensor:
+        if x.is_cuda:
+            return fused_rms_norm(x, self.weight, self.eps)
         return F.rms_norm(x, (self.dim,), self.weight, self.eps)
+
+    def add_forward(self, x: Tensor, residual: Tensor) -> tuple[Tensor, Tensor]:
+        """``(x + residual, norm(x + residual))`` in one pass (device tensors)."""
+        return fused_add_rms_norm(x, residual, self.weight, self.eps)
 
 
 class SwiGLU(nn.Module):
@@ -58,7 +67,13 @@ class SwiGLU(nn.Module):
         self.dropout = nn.Dropout(dropout)
 
     def forward(self, x: Tensor) -> Tensor:
-        return self.dropout(self.down(F.silu(self.gate(x)) * self.up(x)))
+        if not x.is_cuda:
+            return self.dropout(self.down(F.silu(self.gate(x)) * self.up(x)))
+        # One [gate | up] GEMM, then silu(gate) * up in one HIP pass.
+        weight = torch.cat((self.gate.weight, self.up.weight), dim=0)
+        bias = (None if self.gate.bias is None
+                else torch.cat((self.gate.bias, self.up.bias), dim=0))
+        return self.dropout(self.down(fused_swiglu(F.linear(x, weight, bias))))
 
 
 @dataclass
@@ -130,13 +145,29 @@ class BiAttnBlock(nn.Module):
     def forward(self, x: Tensor, valid_mask: Optional[Tensor],
                 seam_reset: Optional[Tensor] = None, path_indices: Optional[Tensor] = None,
                 path_valid: Optional[Tensor] = None) -> Tensor:
+        x, ff = self.forward_pending(x, None, valid_mask, seam_reset, path_indices, path_valid)
+        return x + ff
+
+    def forward_pending(self, x: Tensor, pending: Optional[Tensor], valid_mask: Optional[Tensor],
+                        seam_reset: Optional[Tensor] = None,
+                        path_indices: Optional[Tensor] = None,
+                        path_valid: Optional[Tensor] = None) -> tuple[Tensor, Tensor]:
+        """The block on ``x + pending`` (``pending`` = the previous block's
+        feed-forward output, not yet added), returning ``(x', ff)`` with the
+        block output ``x' + ff`` left unsummed so the next norm can fuse the
+        add.  Each residual add runs inside an RMSNorm pass."""
         layer_paths = None if path_indices is None else path_indices[:, self.layer_index]
         layer_valid = None if path_valid is None else path_valid[:, self.layer_index]
-        x = x + self.attn(self.norm1(x), valid_mask, seam_reset, layer_paths, layer_valid)
-        ff = self.ff(self.norm2(x))
+        if pending is None:
+            normed = self.norm1(x)
+        else:
+            x, normed = self.norm1.add_forward(x, pending)
+        attended = self.attn(normed, valid_mask, seam_reset, layer_paths, layer_valid)
+        x, normed = self.norm2.add_forward(x, attended)
+        ff = self.ff(normed)
         if valid_mask is not None:
             ff = ff * valid_mask[:, :, None].to(x.dtype)
-        return x + ff
+        return x, ff
 
 
 class BiAttnLM(nn.Module):
@@ -200,10 +231,13 @@ class BiAttnLM(nn.Module):
         if valid_mask is not None and bool(valid_mask.all()):
             valid_mask = None
         x = self.drop(self.embedding(input_ids))
+        if path_active is None:
+            pending = None
+            for layer in self.layers:
+                x, pending = layer.forward_pending(x, pending, valid_mask, seam_reset,
+                                                   path_indices, path_valid)
+            return self.norm.add_forward(x, pending)[1]
         for index, layer in enumerate(self.layers):
-            if path_active is None:
-                x = layer(x, valid_mask, seam_reset, path_indices, path_valid)
-                continue
             # Rows whose layer is inactive pass through unchanged (model.py:446-466).
             active = path_active[:, index]
             if not bool(active.any()):

@@ -75,6 +75,16 @@ def _kernel_view(t: torch.Tensor) -> torch.Tensor:
     return t if ok else t.contiguous()
 
 
+def _dense_like(t: torch.Tensor) -> torch.Tensor:
+    """An uninitialised tensor of ``t``'s shape whose memory is dense in
+    ``t``'s stride order -- ``empty_like`` for dense tensors, and for a
+    strided view (q sliced out of a fused QKV projection) the same
+    position-major order instead of PyTorch's contiguous fallback."""
+    order = sorted(range(t.ndim), key=lambda i: -t.stride(i))
+    base = torch.empty([t.shape[i] for i in order], dtype=t.dtype, device=t.device)
+    return base.permute([order.index(i) for i in range(t.ndim)])
+
+
 def _stream(t: torch.Tensor) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
@@ -173,7 +183,7 @@ def sbda_forward(q, k, v, offsets, seg_key=None) -> tuple[torch.Tensor, torch.Te
     _validate(q, k, v, offs, gqa=True)
     lib = _lib.load()
     q, k, v = (_kernel_view(x) for x in (q, k, v))
-    out = torch.empty_like(q)
+    out = _dense_like(q)
     b, h, t, _ = q.shape
     lse = _lse_storage(b, h, t, q.device)
     with torch.cuda.device(q.device):
@@ -195,7 +205,7 @@ def sbda_backward(q, k, v, grad_out, lse, offsets, seg_key=None):
     if lse.shape != q.shape[:3] or lse.dtype != torch.float32:
         raise ValueError("lse must be the fp32 [B,H,T] log-normalisers of the forward")
     lse = _lse_buffer(lse)
-    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dq, dk, dv = _dense_like(q), _dense_like(k), _dense_like(v)
     with torch.cuda.device(q.device):
         _lib.check(lib.sbda_backward(
             _ptr(q), _lib.strides(q), _ptr(k), _lib.strides(k), _ptr(v), _lib.strides(v),
@@ -285,7 +295,7 @@ def sbda_forward_paths(q, k, v, path_indices, path_valid=None, seg_key=None, *, 
     pidx, pval = _paths_check(q, path_indices, path_valid)
     lib = _lib.load()
     q, k, v = (_kernel_view(x) for x in (q, k, v))
-    out = torch.empty_like(q)
+    out = _dense_like(q)
     b, h, t, _ = q.shape
     lse = _lse_storage(b, h, t, q.device)
     with torch.cuda.device(q.device):
@@ -310,7 +320,7 @@ def sbda_backward_paths(q, k, v, grad_out, lse, path_indices, path_valid=None, s
     if lse.shape != q.shape[:3] or lse.dtype != torch.float32:
         raise ValueError("lse must be the fp32 [B,H,T] log-normalisers of the forward")
     lse = _lse_buffer(lse)
-    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dq, dk, dv = _dense_like(q), _dense_like(k), _dense_like(v)
     d = q.shape[-1]
     dwq = dwk = None
     if prologue is not None:
@@ -424,7 +434,7 @@ class _FusedSBDAPrologue(torch.autograd.Function):
         b, h, t, d = q.shape
         wq, wk = _weight32(q_weight, d, q.device), _weight32(k_weight, d, q.device)
         cos, sin = rope_tables(t, d, theta, q.device)
-        out = torch.empty_like(q)
+        out = _dense_like(q)
         lse = _lse_storage(b, h, t, q.device)
         with torch.cuda.device(q.device):
             _lib.check(lib.sbda_forward_prologue(
@@ -444,7 +454,7 @@ class _FusedSBDAPrologue(torch.autograd.Function):
         g = _kernel_view(grad_out)
         if g.dtype != q.dtype:
             g = g.to(q.dtype)
-        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        dq, dk, dv = _dense_like(q), _dense_like(k), _dense_like(v)
         d = q.shape[-1]
         dwq = torch.empty(d, dtype=torch.float32, device=q.device)
         dwk = torch.empty_like(dwq)

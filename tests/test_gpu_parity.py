@@ -689,3 +689,85 @@ def test_backbone_with_tables_and_path_active_matches_oracle():
         scale = pc.grad.abs().max().item() + 1e-8
         err = (p.grad.cpu() - pc.grad).abs().max().item()
         assert err / scale < 1e-3, f"{name}: {err} vs scale {scale}"
+
+
+# ------------------------------------------------------------ block kernels
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, FP32_TOL), (torch.bfloat16, LOW_TOL),
+                                       (torch.float16, LOW_TOL)])
+@pytest.mark.parametrize("dim", [64, 512, 1000, 2048])
+def test_fused_add_rms_norm_matches_fp32_reference(dtype, tol, dim):
+    if dtype == torch.float32 and dim > 2048:
+        pytest.skip("fp32 rows are limited to 8 KiB")
+    g = torch.Generator().manual_seed(dim)
+    x, r, gs, gy = (torch.randn(3, 129, dim, generator=g).to(dtype) for _ in range(4))
+    w = (1 + 0.1 * torch.randn(dim, generator=g)).to(dtype)
+    xd, rd, wd = (t.to(DEV).requires_grad_() for t in (x, r, w))
+    s, y = sbda_amd.fused_add_rms_norm(xd, rd, wd, 1e-6)
+    torch.autograd.backward((s, y), (gs.to(DEV), gy.to(DEV)))
+    # The sum is the eager `x + r` bit for bit.
+    assert torch.equal(s.detach(), x.to(DEV) + r.to(DEV))
+    xc, rc, wc = (t.float().requires_grad_() for t in (x, r, w))
+    sc = (xc + rc).to(dtype).float()                   # eager rounding of the sum
+    yc = torch.nn.functional.rms_norm(sc, (dim,), wc, 1e-6)
+    torch.autograd.backward((sc, yc), (gs.float(), gy.float()))
+    torch.testing.assert_close(y.detach().float().cpu(), yc.detach(), **tol)
+    torch.testing.assert_close(xd.grad.float().cpu(), xc.grad, **tol)
+    torch.testing.assert_close(rd.grad.float().cpu(), rc.grad, **tol)
+    scale = wc.grad.abs().max().item()
+    assert (wd.grad.float().cpu() - wc.grad).abs().max().item() <= 2e-2 * scale + 1e-3
+
+
+def test_fused_rms_norm_alone_and_deterministic_weight_grad():
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(4000, 512, generator=g).to(torch.bfloat16)
+    w = torch.randn(512, generator=g).to(torch.bfloat16)
+    gy = torch.randn(4000, 512, generator=g).to(torch.bfloat16)
+    grads = []
+    for _ in range(2):
+        xd, wd = x.to(DEV).requires_grad_(), w.to(DEV).requires_grad_()
+        y = sbda_amd.fused_rms_norm(xd, wd)
+        y.backward(gy.to(DEV))
+        grads.append((y.detach().cpu(), xd.grad.cpu(), wd.grad.cpu()))
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
+    yc = torch.nn.functional.rms_norm(x.float(), (512,), w.float(), 1e-6)
+    torch.testing.assert_close(grads[0][0].float(), yc, **LOW_TOL)
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, FP32_TOL), (torch.bfloat16, LOW_TOL)])
+@pytest.mark.parametrize("hidden", [64, 200, 2048])
+def test_fused_swiglu_matches_fp32_reference(dtype, tol, hidden):
+    g = torch.Generator().manual_seed(hidden)
+    gu = (2 * torch.randn(5, 77, 2 * hidden, generator=g)).to(dtype)
+    dh = torch.randn(5, 77, hidden, generator=g).to(dtype)
+    gud = gu.to(DEV).requires_grad_()
+    h = sbda_amd.fused_swiglu(gud)
+    h.backward(dh.to(DEV))
+    guc = gu.float().requires_grad_()
+    hc = torch.nn.functional.silu(guc[..., :hidden]) * guc[..., hidden:]
+    hc.backward(dh.float())
+    torch.testing.assert_close(h.detach().float().cpu(), hc.detach(), **tol)
+    torch.testing.assert_close(gud.grad.float().cpu(), guc.grad, **tol)
+
+
+def test_bf16_backbone_tracks_the_fp32_oracle_composition():
+    # The config-5 layer shape (d=512, 8 x 64 heads, FFN 2048) in bf16 on the
+    # GPU -- fused QKV GEMM, add+RMSNorm and SwiGLU kernels -- against the same
+    # weights in fp32 through the oracle on the CPU.
+    torch.manual_seed(62)
+    cfg = sbda_amd.BiAttnConfig(vocab_size=256, dim=512, layers=3, heads=8, ff_hidden=2048)
+    m = sbda_amd.BiAttnLM(cfg)
+    ids = torch.randint(0, 256, (1, 700))
+    md = sbda_amd.BiAttnLM(cfg)
+    md.load_state_dict(m.state_dict())
+    md = md.to(device=DEV, dtype=torch.bfloat16)
+    with torch.no_grad():
+        got = md.forward_hidden(ids.to(DEV)).float().cpu()
+        x = m.embedding(ids)
+        for blk in m.layers:
+            x = x + _oracle_module_forward(blk.attn, blk.norm1(x))
+            x = x + blk.ff(blk.norm2(x))
+        want = m.norm(x)
+    rel = ((got - want).norm() / want.norm()).item()
+    assert rel < 2e-2, rel

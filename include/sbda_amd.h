@@ -93,9 +93,19 @@ int sbda_forward(const void* q, const int64_t* q_strides,
                  const int32_t* offsets, int32_t num_offsets,
                  const int32_t* seg_key, void* stream);
 
+/* Workspace bytes sbda_backward needs for these shapes and masks (0 for the
+ * wavefront-walk kernels; < 0: error). */
+int64_t sbda_backward_workspace(int64_t batch, int64_t heads, int64_t kv_heads,
+                                int64_t length, int64_t head_dim, int32_t dtype,
+                                const int32_t* offsets, int32_t num_offsets,
+                                const int32_t* seg_key);
+
 /*
  * Backward from the forward's saved q, k, v and lse.  Writes dq, dk, dv (each
- * row exactly once: deterministic, no atomics).
+ * row exactly once: deterministic, no atomics).  `workspace` (16-byte
+ * aligned, sbda_backward_workspace bytes; may be NULL when that is 0) holds
+ * the per-(row, slot) weights that the generic kernels pass from their query
+ * pass to their key pass.
  */
 int sbda_backward(const void* q, const int64_t* q_strides,
                   const void* k, const int64_t* k_strides,
@@ -105,6 +115,7 @@ int sbda_backward(const void* q, const int64_t* q_strides,
                   void* dq, const int64_t* dq_strides,
                   void* dk, const int64_t* dk_strides,
                   void* dv, const int64_t* dv_strides,
+                  void* workspace, int64_t workspace_bytes,
                   int64_t batch, int64_t heads, int64_t kv_heads,
                   int64_t length, int64_t head_dim, int32_t dtype,
                   const int32_t* offsets, int32_t num_offsets,

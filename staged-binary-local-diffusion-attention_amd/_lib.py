@@ -11,7 +11,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("libsbda_amd.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 OK, ERR_VALUE, ERR_DTYPE, ERR_RUNTIME = 0, 1, 2, 3
 _ERRORS = {ERR_VALUE: ValueError, ERR_DTYPE: TypeError, ERR_RUNTIME: RuntimeError}
@@ -33,8 +33,9 @@ SIGNATURES = {
     "sbda_last_error": (ctypes.c_char_p, []),
     "sbda_forward": (ctypes.c_int, [_p, _strides, _p, _strides, _p, _strides, _p, _strides,
                                     _fptr, *_SHAPE, _SEG, _p]),
+    "sbda_backward_workspace": (ctypes.c_int64, [*_SHAPE, _SEG]),
     "sbda_backward": (ctypes.c_int, [_p, _strides, _p, _strides, _p, _strides, _p, _strides,
-                                     _fptr, _p, _strides, _p, _strides, _p, _strides,
+                                     _fptr, _p, _strides, _p, _strides, _p, _strides, _p, _i64,
                                      *_SHAPE, _SEG, _p]),
     "sbda_forward_prologue": (ctypes.c_int, [_p, _strides, _p, _strides, _p, _strides, _p,
                                              _strides, _fptr, _fptr, _fptr, _p, _p, _f32,

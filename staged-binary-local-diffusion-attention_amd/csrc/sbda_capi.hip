@@ -13,7 +13,8 @@ namespace sbda {
 
 hipError_t direct_forward(const Params& p, int dtype, bool pro, hipStream_t st);
 hipError_t direct_backward(const Params& p, int dtype, bool pro, hipStream_t st);
-void direct_partials(const Params& p, int esz, int64_t* parts_q, int64_t* parts_k);
+void direct_partials(const Params& p, int esz, int64_t* parts_q, int64_t* parts_k,
+                     int64_t* tab_floats);
 bool walk_applies(const Params& p, int dtype);
 hipError_t walk_forward(const Params& p, int dtype, bool pro, hipStream_t st);
 hipError_t walk_backward(const Params& p, int dtype, bool pro, hipStream_t st);
@@ -184,14 +185,20 @@ int forward_impl(bool pro, const void* q, const int64_t* qs, const void* k, cons
   return hip_status(e, "sbda forward launch");
 }
 
-// Workspace of the prologue backward: weight-gradient partial rows for the
-// query and key sides, then (walk kernels) the per-(row, slot) weight table.
-void partials(const Params& p, int dtype, int64_t* pq, int64_t* pk, int64_t* tab) {
-  *tab = 0;
-  if (walk_applies(p, dtype))
-    walk_partials(p, dtype, pq, pk, tab);
-  else
-    direct_partials(p, esize(dtype), pq, pk);
+// Workspace of the backward, in floats: weight-gradient partial rows for the
+// query and key sides (prologue only), then the per-(row, slot) weight table
+// (generic kernels, and the walk kernels' two-pass prologue backward).
+int64_t workspace_floats(const Params& p, int dtype, bool pro, int64_t* pq, int64_t* pk) {
+  int64_t tab = 0;
+  *pq = *pk = 0;
+  if (walk_applies(p, dtype)) {
+    if (!pro) return 0;
+    walk_partials(p, dtype, pq, pk, &tab);
+  } else {
+    direct_partials(p, esize(dtype), pq, pk, &tab);
+    if (!pro) *pq = *pk = 0;
+  }
+  return (*pq + *pk) * p.D + tab;
 }
 
 int backward_impl(bool pro, const void* q, const int64_t* qs, const void* k, const int64_t* ks,
@@ -219,24 +226,25 @@ int backward_impl(bool pro, const void* q, const int64_t* qs, const void* k, con
   p.lse = const_cast<float*>(lse);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   int64_t pq = 0, pk = 0;
-  if (pro) {
-    if (!wq || !wk || !rc || !rs || !dwq || !dwk)
-      return fail(SBDA_ERR_VALUE, "prologue: null weight, weight-gradient or RoPE table");
-    int64_t tab = 0;
-    partials(p, dtype, &pq, &pk, &tab);
-    const int64_t need = ((pq + pk) * p.D + tab) * (int64_t)sizeof(float);
+  if (pro && (!wq || !wk || !rc || !rs || !dwq || !dwk))
+    return fail(SBDA_ERR_VALUE, "prologue: null weight, weight-gradient or RoPE table");
+  const int64_t need = workspace_floats(p, dtype, pro, &pq, &pk) * (int64_t)sizeof(float);
+  if (need > 0) {
     if (ws == nullptr || ws_bytes < need)
-      return fail(SBDA_ERR_VALUE, "prologue backward: workspace of %lld bytes needed, %lld given",
+      return fail(SBDA_ERR_VALUE, "backward: workspace of %lld bytes needed, %lld given",
                   (long long)need, (long long)ws_bytes);
-    if (reinterpret_cast<uintptr_t>(ws) % 16) return fail(SBDA_ERR_VALUE, "workspace must be 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(ws) % 16)
+      return fail(SBDA_ERR_VALUE, "workspace must be 16-byte aligned");
+    p.dwq_part = reinterpret_cast<float*>(ws);
+    p.dwk_part = p.dwq_part + pq * p.D;
+    p.tab = p.dwk_part + pk * p.D;
+  }
+  if (pro) {
     p.wq = wq;
     p.wk = wk;
     p.rope_cos = rc;
     p.rope_sin = rs;
     p.eps = eps;
-    p.dwq_part = reinterpret_cast<float*>(ws);
-    p.dwk_part = p.dwq_part + pq * p.D;
-    p.tab = p.dwk_part + pk * p.D;
   }
   hipError_t e = walk_applies(p, dtype) ? walk_backward(p, dtype, pro, st)
                                         : direct_backward(p, dtype, pro, st);
@@ -352,7 +360,7 @@ using namespace sbda;
 
 extern "C" {
 
-int sbda_abi_version(void) { return 6; }
+int sbda_abi_version(void) { return 7; }
 
 const char* sbda_last_error(void) { return g_error.c_str(); }
 
@@ -365,15 +373,28 @@ int sbda_forward(const void* q, const int64_t* qs, const void* k, const int64_t*
                       stream);
 }
 
+int64_t sbda_backward_workspace(int64_t batch, int64_t heads, int64_t kv_heads, int64_t length,
+                                int64_t head_dim, int32_t dtype, const int32_t* offsets,
+                                int32_t n, const int32_t* seg_key) {
+  g_error.clear();
+  Params p;
+  int rc = check_problem(batch, heads, kv_heads, length, head_dim, dtype, offsets, n, p);
+  if (rc) return -rc;
+  p.seg = seg_key;
+  int64_t pq = 0, pk = 0;
+  return workspace_floats(p, dtype, false, &pq, &pk) * (int64_t)sizeof(float);
+}
+
 int sbda_backward(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
                   const int64_t* vs, const void* dout, const int64_t* dos, const float* lse, void* dq,
                   const int64_t* dqs, void* dk, const int64_t* dks, void* dv, const int64_t* dvs,
-                  int64_t batch, int64_t heads, int64_t kv_heads, int64_t length, int64_t head_dim,
-                  int32_t dtype, const int32_t* offsets, int32_t n, const int32_t* seg_key,
-                  void* stream) {
+                  void* workspace, int64_t workspace_bytes, int64_t batch, int64_t heads,
+                  int64_t kv_heads, int64_t length, int64_t head_dim, int32_t dtype,
+                  const int32_t* offsets, int32_t n, const int32_t* seg_key, void* stream) {
   return backward_impl(false, q, qs, k, ks, v, vs, dout, dos, lse, nullptr, nullptr, nullptr, nullptr,
-                       0.f, dq, dqs, dk, dks, dv, dvs, nullptr, nullptr, nullptr, 0, batch, heads,
-                       kv_heads, length, head_dim, dtype, offsets, n, seg_key, stream);
+                       0.f, dq, dqs, dk, dks, dv, dvs, nullptr, nullptr, workspace,
+                       workspace_bytes, batch, heads, kv_heads, length, head_dim, dtype, offsets, n,
+                       seg_key, stream);
 }
 
 int sbda_forward_prologue(const void* q, const int64_t* qs, const void* k, const int64_t* ks,
@@ -396,9 +417,8 @@ int64_t sbda_backward_prologue_workspace(int64_t batch, int64_t heads, int64_t k
   int rc = check_problem(batch, heads, kv_heads, length, head_dim, dtype, offsets, n, p);
   if (rc) return -rc;
   p.seg = seg_key;
-  int64_t pq = 0, pk = 0, tab = 0;
-  partials(p, dtype, &pq, &pk, &tab);
-  return ((pq + pk) * p.D + tab) * (int64_t)sizeof(float);
+  int64_t pq = 0, pk = 0;
+  return workspace_floats(p, dtype, true, &pq, &pk) * (int64_t)sizeof(float);
 }
 
 int sbda_backward_prologue(const void* q, const int64_t* qs, const void* k, const int64_t* ks,

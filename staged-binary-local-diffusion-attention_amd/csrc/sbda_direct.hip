@@ -16,6 +16,12 @@
 //   dK_j = scale sum_{h in group} sum_t dS_t(i = j + off[t]) q_i   (i < T),
 //   dV_j =       sum_{h in group} sum_t p_t(i = j + off[t]) dO_i.
 // A row with no valid source has o = 0, gradient 0 and lse = +inf.
+//
+// Backward in two passes, neither with atomics: bwd_dq_direct computes each
+// query row's p_s and dS_s once, writes dQ and stores (p_s, scale * dS_s) in
+// a workspace table; bwd_dkv_direct sums, per kv row j, the table entries of
+// the queries j + off[t] (over the group's query heads) against their q and
+// dO rows.
 
 #include "sbda_rows.h"
 
@@ -158,6 +164,13 @@ __global__ __launch_bounds__(kBlock) void bwd_dq_direct(Params p) {
       if (s < p.S) a = __builtin_fmaf(ds[s], kk[s][e], a);
     dq[e] = a * p.scale;
   }
+  // (p_s, scale * dS_s) of this row for the key pass.
+  if (live && li == 0) {
+    float2* tab = reinterpret_cast<float2*>(p.tab) + row * p.S;
+#pragma unroll
+    for (int s = 0; s < kMaxSlots; ++s)
+      if (s < p.S) tab[s] = make_float2(pp[s], ds[s] * p.scale);
+  }
   if constexpr (PRO) {
     using PL = Prologue<T, LPR>;
     float x[VEC], c[PL::HV], s[PL::HV], dw[VEC];
@@ -193,6 +206,9 @@ __global__ __launch_bounds__(kBlock) void bwd_dkv_direct(Params p) {
   int b, j, hk;
   decode_row(row, p.Hkv, p.T, b, j, hk);
 
+  // Query i = j + off[t] reads key j through slot t; its weight p_t and
+  // scale * dS_t come from the table the dQ pass wrote.
+  const float2* tab = reinterpret_cast<const float2*>(p.tab);
   float dk[VEC], dv[VEC];
 #pragma unroll
   for (int e = 0; e < VEC; ++e) { dk[e] = 0.f; dv[e] = 0.f; }
@@ -204,18 +220,21 @@ __global__ __launch_bounds__(kBlock) void bwd_dkv_direct(Params p) {
         const int64_t i64 = (int64_t)j + p.off[tslot];
         const bool ok = i64 < p.T;
         const int i = ok ? (int)i64 : j;
-        float q[VEC], go[VEC], pp[kMaxSlots], ds[kMaxSlots], kk[kMaxSlots][VEC];
-        query_side<T, LPR, PRO, false>(p, b, i, h, hk, li, q, go, pp, ds, kk);
-        float pt = 0.f, dst = 0.f;
-#pragma unroll
-        for (int s = 0; s < kMaxSlots; ++s)
-          if (s == tslot) { pt = pp[s]; dst = ds[s]; }
-        if (!ok) { pt = 0.f; dst = 0.f; }
-        dst *= p.scale;
+        float2 w = tab[(((int64_t)b * p.T + i) * p.H + h) * p.S + tslot];
+        if (!ok) w = make_float2(0.f, 0.f);
+        float q[VEC], go[VEC];
+        load_row<T, PRO>(row_ptr<T>(p.q, b, h, i), li, p.D, q);
+        if constexpr (PRO) {
+          using PL = Prologue<T, LPR>;
+          float c[PL::HV], sn[PL::HV];
+          PL::load_cs(p.rope_cos, p.rope_sin, i, li, p.D, c, sn);
+          PL::forward(q, p.wq, c, sn, li, p.D, p.eps);
+        }
+        load_row<T, PRO>(row_ptr<T>(p.dout, b, h, i), li, p.D, go);
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
-          dk[e] = __builtin_fmaf(dst, q[e], dk[e]);
-          dv[e] = __builtin_fmaf(pt, go[e], dv[e]);
+          dk[e] = __builtin_fmaf(w.y, q[e], dk[e]);
+          dv[e] = __builtin_fmaf(w.x, go[e], dv[e]);
         }
       }
     }
@@ -301,7 +320,11 @@ hipError_t direct_backward(const Params& p, int dtype, bool pro, hipStream_t st)
   }
 }
 
-void direct_partials(const Params& p, int esz, int64_t* parts_q, int64_t* parts_k) {
+// Workspace of the generic backward: weight-gradient partial rows (with the
+// prologue) and the (p, scale * dS) table, fp32 pairs per (row, slot).
+void direct_partials(const Params& p, int esz, int64_t* parts_q, int64_t* parts_k,
+                     int64_t* tab_floats) {
+  *tab_floats = (int64_t)p.B * p.T * p.H * 2 * p.S;
   const int lpr = lanes_per_row(p.D, esz);
   const int64_t qrows = (int64_t)p.B * p.T * p.H;
   const int64_t krows = (int64_t)p.B * p.T * p.Hkv;

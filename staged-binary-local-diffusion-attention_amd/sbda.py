@@ -206,12 +206,18 @@ def sbda_backward(q, k, v, grad_out, lse, offsets, seg_key=None):
         raise ValueError("lse must be the fp32 [B,H,T] log-normalisers of the forward")
     lse = _lse_buffer(lse)
     dq, dk, dv = _dense_like(q), _dense_like(k), _dense_like(v)
+    shape = _shape_args(q, k, offs)
+    seg = _seg_arg(seg_key, q)
+    need = lib.sbda_backward_workspace(*shape, seg)
+    if need < 0:
+        _lib.check(-need)
+    ws = torch.empty(int(need), dtype=torch.uint8, device=q.device) if need else None
     with torch.cuda.device(q.device):
         _lib.check(lib.sbda_backward(
             _ptr(q), _lib.strides(q), _ptr(k), _lib.strides(k), _ptr(v), _lib.strides(v),
             _ptr(grad_out), _lib.strides(grad_out), _ptr(lse),
             _ptr(dq), _lib.strides(dq), _ptr(dk), _lib.strides(dk), _ptr(dv), _lib.strides(dv),
-            *_shape_args(q, k, offs), _seg_arg(seg_key, q), _stream(q)))
+            _ptr(ws), 0 if ws is None else ws.numel(), *shape, seg, _stream(q)))
     return dq, dk, dv
 
 

@@ -7,20 +7,28 @@
 //
 // Sources.  Offsets split into "near" ones (0, 1, 2: a compile-time mask NM)
 // and at most one "far" offset F >= 3.  Near sources are the rows the walk
-// just loaded, kept in a 3-deep register rotation (no reload); the far
-// source is loaded directly.  Tiles are ordered so that the wave holding
-// positions t - F (and t + F) runs next to this one -- linear order for
-// F < P, column order (tile a, a + F, a + 2F, ...) otherwise -- and the
-// workgroup id is remapped so consecutive tiles share an XCD (and its L2).
+// just loaded, kept in a register rotation (no reload).  Tiles are ordered so
+// that the tile holding positions t - F (and t + F) is walked next to this
+// one -- linear order for F < P, column order (tile a, a + F, a + 2F, ...)
+// otherwise -- and the workgroup id is remapped so consecutive tiles share
+// an XCD (and its L2).
+//
+// Forward: per position, scores against the near rows and the far row
+// (loaded directly), softmax, O and one log-normaliser per row.
 //
 // Backward (gather form, every row written once, no atomics).  Walking
 // queries u = a-2 .. end+1, the wave computes each query's weights p_s and
-// score gradients dS_s once; dQ_u is complete at once, and near-slot
-// contributions dK/dV_{u-n} += (scale dS_n q_u, p_n dO_u) go to three
-// rotating key accumulators.  Key j = u-2 is then complete except for its
-// far query i = j + F, whose weights are recomputed from q_i, dO_i, lse_i and
-// i's own sources (a second rotation over positions i, i-1, i-2, plus k_j,
-// v_j from the first).  Keys are written as soon as they complete.
+// score gradients dS_s once from its lse; dQ_u is complete at once.  Key
+// j = u-2 is then finalised from queries j, j+1, j+2 (near slots, kept in the
+// rotation) and its far query i = j + F.  In column order a workgroup of
+// waves walks consecutive rows of the column in lockstep and passes rows and
+// the far slot's weights through LDS (bwd_chain); otherwise the far query's
+// weights are recomputed from q_i, dO_i, lse_i and i's own sources (bwd_pipe).
+// Keys are written as soon as they complete.
+//
+// Addressing.  Row addresses are formed from a wave-uniform row offset and a
+// constant per-lane offset (Stream), so the loops carry no per-lane 64-bit
+// arithmetic.
 //
 // Reference semantics: BiAttn/left_v2.py:313-405 (forward maths) and the
 // key-centric backward specified by BiAttn/sbda_triton.py:507-671.
@@ -36,6 +44,17 @@ namespace {
 
 constexpr int kWaves = 4;               // independent waves per workgroup
 constexpr int kWalkBlock = kWaves * 64;
+
+// Tiles per launch the tile size aims for (at least).
+constexpr int kWalkTiles = 8192;
+
+// The forward walks are launched with this much (unused) LDS per workgroup so
+// that at most two 4-wave workgroups share a CU (2 waves per SIMD).  Measured
+// at T = 2^20: the forward runs ~4% faster than at the 4-7 waves per SIMD its
+// registers allow (fewer concurrent row streams per HBM channel); 1 or 3-4
+// waves per SIMD are slower.  The backward walks are register-limited to 2-4
+// waves per SIMD already and gain nothing from a cap.
+constexpr unsigned kFwdLdsCap = 65536;
 
 struct WalkCfg {
   int P;         // positions per tile
@@ -75,82 +94,6 @@ __device__ inline bool decode_tile(const Params& p, const WalkCfg& c, int64_t n,
   return a < p.T;
 }
 
-template <typename T>
-struct Rows {
-  const T* __restrict__ base;
-  int64_t st;
-  __device__ inline const T* at(int64_t t) const { return base + t * st; }
-};
-
-template <typename T, int LPR, bool PRO>
-struct Lane {
-  static constexpr int VEC = VecOf<T>::value;
-  using PL = Prologue<T, LPR>;
-  int li;
-  int D;
-  const float* wq;
-  const float* wk;
-  const float* rc;
-  const float* rs;
-  float eps;
-
-  __device__ inline void init(const Params& p, int lane_in_row) {
-    li = lane_in_row;
-    D = p.D;
-    wq = p.wq;
-    wk = p.wk;
-    rc = p.rope_cos;
-    rs = p.rope_sin;
-    eps = p.eps;
-  }
-
-  __device__ inline void load(const Rows<T>& r, int64_t t, float (&x)[VEC]) const {
-    load_row<T, PRO>(r.at(t), li, D, x);
-  }
-  __device__ inline void zero(float (&x)[VEC]) const {
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) x[i] = 0.f;
-  }
-  // Loads a q or k row and, with the prologue, normalises and rotates it.
-  __device__ inline void load_qk(const Rows<T>& r, int64_t t, const float* w, float (&x)[VEC]) const {
-    load(r, t, x);
-    if constexpr (PRO) {
-      float c[PL::HV], s[PL::HV];
-      PL::load_cs(rc, rs, t, li, D, c, s);
-      PL::forward(x, w, c, s, li, D, eps);
-    }
-  }
-  __device__ inline float dot(const float (&a)[VEC], const float (&b)[VEC]) const {
-    return row_sum<LPR>(dot_partial<VEC>(a, b));
-  }
-};
-
-// Weights and score gradients of one query from its sources.
-template <int NS, int VEC, int LPR>
-__device__ inline void query_grads(const float (&q)[VEC], const float (&go)[VEC], float lse,
-                                   float scale, const float* const (&ks)[NS],
-                                   const float* const (&vs)[NS], const bool (&ok)[NS],
-                                   float (&pp)[NS], float (&ds)[NS]) {
-  float dp[NS];
-  float delta = 0.f;
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    float a = 0.f, d = 0.f;
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      a = __builtin_fmaf(q[e], ks[s][e], a);
-      d = __builtin_fmaf(go[e], vs[s][e], d);
-    }
-    a = row_sum<LPR>(a) * scale;
-    d = row_sum<LPR>(d);
-    pp[s] = ok[s] ? fast_exp(a - lse) : 0.f;
-    dp[s] = d;
-    delta = __builtin_fmaf(pp[s], d, delta);
-  }
-#pragma unroll
-  for (int s = 0; s < NS; ++s) ds[s] = pp[s] * (dp[s] - delta);
-}
-
 template <int NM>
 struct NearSet {
   static constexpr bool has0 = NM & 1, has1 = NM & 2, has2 = NM & 4;
@@ -164,309 +107,6 @@ struct NearSet {
         ++seen;
       }
     return -1;
-  }
-};
-
-// =================================================================== forward
-
-template <typename T, int LPR, int NM, bool FAR, bool PRO>
-struct FwdWalker {
-  static constexpr int VEC = VecOf<T>::value;
-  static constexpr int NN = NearSet<NM>::count;
-  static constexpr int NS = NN + (FAR ? 1 : 0);
-  using L = Lane<T, LPR, PRO>;
-
-  L ln;
-  Rows<T> q, k, v;
-  T* __restrict__ o;
-  int64_t ost;
-  float* __restrict__ lse;
-  int lst;
-  float scale;
-  int F;
-  float kr[3][VEC], vr[3][VEC];
-
-  template <int R>
-  __device__ inline void step(int t) {
-    ln.load_qk(k, t, ln.wk, kr[R]);
-    ln.load(v, t, vr[R]);
-    float qr[VEC];
-    ln.load_qk(q, t, ln.wq, qr);
-    const int tf = t - F;
-    float kf[VEC], vf[VEC];
-    if constexpr (FAR) {
-      if (tf >= 0) {
-        ln.load_qk(k, tf, ln.wk, kf);
-        ln.load(v, tf, vf);
-      } else {
-        ln.zero(kf);
-        ln.zero(vf);
-      }
-    }
-    float sc[NS];
-    bool ok[NS];
-    const float* vs[NS];
-    int idx = 0;
-#pragma unroll
-    for (int n = 0; n < 3; ++n) {
-      if (NM & (1 << n)) {
-        const int slot = (R + 3 - n) % 3;
-        ok[idx] = t - n >= 0;
-        sc[idx] = ln.dot(qr, kr[slot]) * scale;
-        vs[idx] = vr[slot];
-        ++idx;
-      }
-    }
-    if constexpr (FAR) {
-      ok[NS - 1] = tf >= 0;
-      sc[NS - 1] = ln.dot(qr, kf) * scale;
-      vs[NS - 1] = vf;
-    }
-    float m = -INFINITY;
-#pragma unroll
-    for (int s = 0; s < NS; ++s)
-      if (ok[s]) m = fmaxf(m, sc[s]);
-    float acc[VEC];
-    ln.zero(acc);
-    float l = 0.f;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const float w = ok[s] ? fast_exp(sc[s] - m) : 0.f;
-      l += w;
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) acc[e] = __builtin_fmaf(w, vs[s][e], acc[e]);
-    }
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) acc[e] *= inv;
-    store_row<T, PRO>(o + (int64_t)t * ost, ln.li, ln.D, acc);
-    if (ln.li == 0) lse[(int64_t)t * lst] = l > 0.f ? m + fast_log(l) : INFINITY;
-  }
-
-  // Loads position t's k/v into rotation slot R (zeros before the start).
-  template <int R>
-  __device__ inline void prefill(int t) {
-    if (t >= 0) {
-      ln.load_qk(k, t, ln.wk, kr[R]);
-      ln.load(v, t, vr[R]);
-    } else {
-      ln.zero(kr[R]);
-      ln.zero(vr[R]);
-    }
-  }
-};
-
-template <typename T, int LPR, int NM, bool FAR, bool PRO>
-__global__ __launch_bounds__(kWalkBlock) void fwd_walk(Params p, WalkCfg c) {
-  int b, hg, a;
-  if (!decode_tile(p, c, wave_id(), b, hg, a)) return;
-  const int lane = threadIdx.x & 63;
-  const int h = hg * (64 / LPR) + lane / LPR;
-  FwdWalker<T, LPR, NM, FAR, PRO> w;
-  w.ln.init(p, lane % LPR);
-  w.q = {reinterpret_cast<const T*>(p.q.p) + (int64_t)b * p.q.sb + (int64_t)h * p.q.sh, p.q.st};
-  w.k = {reinterpret_cast<const T*>(p.k.p) + (int64_t)b * p.k.sb + (int64_t)h * p.k.sh, p.k.st};
-  w.v = {reinterpret_cast<const T*>(p.v.p) + (int64_t)b * p.v.sb + (int64_t)h * p.v.sh, p.v.st};
-  w.o = reinterpret_cast<T*>(p.o.p) + (int64_t)b * p.o.sb + (int64_t)h * p.o.sh;
-  w.ost = p.o.st;
-  w.lse = p.lse + (int64_t)b * p.T * p.H + h;
-  w.lst = p.H;
-  w.scale = p.scale;
-  w.F = c.F;
-  const int end = min(a + c.P, p.T);
-  // Rotation slot of position t is (t - a) mod 3: a-1 -> 2, a-2 -> 1.
-  if constexpr ((NM & 6) != 0) {
-    w.template prefill<2>(a - 1);
-    w.template prefill<1>(a - 2);
-  }
-  int t = a;
-  for (; t + 3 <= end; t += 3) {
-    w.template step<0>(t);
-    w.template step<1>(t + 1);
-    w.template step<2>(t + 2);
-  }
-  if (t < end) w.template step<0>(t);
-  if (t + 1 < end) w.template step<1>(t + 1);
-}
-
-// ================================================================== backward
-
-template <typename T, int LPR, int NM, bool FAR, bool PRO>
-struct BwdWalker {
-  static constexpr int VEC = VecOf<T>::value;
-  static constexpr int NN = NearSet<NM>::count;
-  static constexpr int NS = NN + (FAR ? 1 : 0);
-  using L = Lane<T, LPR, PRO>;
-  using PL = Prologue<T, LPR>;
-
-  L ln;
-  Rows<T> q, k, v, go;
-  T* __restrict__ dq;
-  T* __restrict__ dk;
-  T* __restrict__ dv;
-  int64_t dqst, dkst, dvst;
-  const float* __restrict__ lse;
-  int lst;
-  float scale;
-  int F, T_, a, end, qend;
-  float kr[3][VEC], vr[3][VEC];     // own rotation: k, v at u (slot R), u-1, u-2
-  float fk[3][VEC], fv[3][VEC];     // far-right rotation: i = u-2+F, i-1, i-2
-  float ak[3][VEC], av[3][VEC];     // key accumulators: keys u, u-1, u-2
-  float dwq[VEC], dwk[VEC];         // prologue weight-gradient partials
-
-  template <int R>
-  __device__ inline void step(int u) {
-    constexpr int R1 = (R + 2) % 3;   // slot of u-1
-    constexpr int R2 = (R + 1) % 3;   // slot of u-2
-    // 1. Own rotation push and fresh accumulator for key u.
-    if (u >= 0 && u < T_) {
-      ln.load_qk(k, u, ln.wk, kr[R]);
-      ln.load(v, u, vr[R]);
-    } else {
-      ln.zero(kr[R]);
-      ln.zero(vr[R]);
-    }
-    ln.zero(ak[R]);
-    ln.zero(av[R]);
-    // 2. Far-right rotation push: position u - 2 + F.
-    if constexpr (FAR) {
-      const int i = u - 2 + F;
-      if (i >= 0 && i < T_) {
-        ln.load_qk(k, i, ln.wk, fk[R]);
-        ln.load(v, i, fv[R]);
-      } else {
-        ln.zero(fk[R]);
-        ln.zero(fv[R]);
-      }
-    }
-    // 3. Own query u.
-    if (u >= a && u < qend) {
-      float qr[VEC], gr[VEC], xq[VEC];
-      float rq = 0.f, cq[PL::HV], sq[PL::HV];
-      ln.load(q, u, xq);
-      if constexpr (PRO) {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) qr[e] = xq[e];
-        PL::load_cs(ln.rc, ln.rs, u, ln.li, ln.D, cq, sq);
-        rq = PL::forward(qr, ln.wq, cq, sq, ln.li, ln.D, ln.eps);
-      } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) qr[e] = xq[e];
-      }
-      ln.load(go, u, gr);
-      const float l = lse[(int64_t)u * lst];
-      float kf[VEC], vf[VEC];
-      const int uf = u - F;
-      if constexpr (FAR) {
-        if (uf >= 0) {
-          ln.load_qk(k, uf, ln.wk, kf);
-          ln.load(v, uf, vf);
-        } else {
-          ln.zero(kf);
-          ln.zero(vf);
-        }
-      }
-      const float* ks[NS];
-      const float* vs[NS];
-      bool ok[NS];
-      int idx = 0;
-#pragma unroll
-      for (int n = 0; n < 3; ++n) {
-        if (NM & (1 << n)) {
-          const int slot = (R + 3 - n) % 3;
-          ks[idx] = kr[slot];
-          vs[idx] = vr[slot];
-          ok[idx] = u - n >= 0;
-          ++idx;
-        }
-      }
-      if constexpr (FAR) {
-        ks[NS - 1] = kf;
-        vs[NS - 1] = vf;
-        ok[NS - 1] = uf >= 0;
-      }
-      float pp[NS], ds[NS];
-      query_grads<NS, VEC, LPR>(qr, gr, l, scale, ks, vs, ok, pp, ds);
-      if (u < end) {
-        float g[VEC];
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          float acc = 0.f;
-#pragma unroll
-          for (int s = 0; s < NS; ++s) acc = __builtin_fmaf(ds[s], ks[s][e], acc);
-          g[e] = acc * scale;
-        }
-        if constexpr (PRO) PL::backward(g, xq, rq, ln.wq, cq, sq, ln.li, ln.D, dwq);
-        store_row<T, PRO>(dq + (int64_t)u * dqst, ln.li, ln.D, g);
-      }
-      // Near-slot contributions to keys u - n.
-      idx = 0;
-#pragma unroll
-      for (int n = 0; n < 3; ++n) {
-        if (NM & (1 << n)) {
-          const int slot = (R + 3 - n) % 3;
-          const float cs = ds[idx] * scale, cp = pp[idx];
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) {
-            ak[slot][e] = __builtin_fmaf(cs, qr[e], ak[slot][e]);
-            av[slot][e] = __builtin_fmaf(cp, gr[e], av[slot][e]);
-          }
-          ++idx;
-        }
-      }
-    }
-    // 4. Key j = u - 2 is complete but for its far query i = j + F.
-    const int j = u - 2;
-    if (j >= a && j < end) {
-      if constexpr (FAR) {
-        const int i = j + F;
-        if (i < T_) {
-          float qr[VEC], gr[VEC];
-          ln.load_qk(q, i, ln.wq, qr);
-          ln.load(go, i, gr);
-          const float l = lse[(int64_t)i * lst];
-          const float* ks[NS];
-          const float* vs[NS];
-          bool ok[NS];
-          int idx = 0;
-#pragma unroll
-          for (int n = 0; n < 3; ++n) {
-            if (NM & (1 << n)) {
-              const int slot = (R + 3 - n) % 3;
-              ks[idx] = fk[slot];
-              vs[idx] = fv[slot];
-              ok[idx] = true;   // i - n >= F - 2 > 0
-              ++idx;
-            }
-          }
-          ks[NS - 1] = kr[R2];
-          vs[NS - 1] = vr[R2];
-          ok[NS - 1] = true;
-          float pp[NS], ds[NS];
-          query_grads<NS, VEC, LPR>(qr, gr, l, scale, ks, vs, ok, pp, ds);
-          const float cs = ds[NS - 1] * scale, cp = pp[NS - 1];
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) {
-            ak[R2][e] = __builtin_fmaf(cs, qr[e], ak[R2][e]);
-            av[R2][e] = __builtin_fmaf(cp, gr[e], av[R2][e]);
-          }
-        }
-      }
-      if constexpr (PRO) {
-        float xk[VEC], c[PL::HV], s[PL::HV];
-        ln.load(k, j, xk);
-        PL::load_cs(ln.rc, ln.rs, j, ln.li, ln.D, c, s);
-        float ss = 0.f;
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) ss = __builtin_fmaf(xk[e], xk[e], ss);
-        ss = row_sum<LPR>(ss);
-        const float r = __builtin_amdgcn_rsqf(__fadd_rn(__fdiv_rn(ss, (float)ln.D), ln.eps));
-        PL::backward(ak[R2], xk, r, ln.wk, c, s, ln.li, ln.D, dwk);
-      }
-      store_row<T, PRO>(dk + (int64_t)j * dkst, ln.li, ln.D, ak[R2]);
-      store_row<T, PRO>(dv + (int64_t)j * dvst, ln.li, ln.D, av[R2]);
-    }
-    (void)R1;
   }
 };
 
@@ -492,62 +132,10 @@ __device__ inline void write_wave_partial(float (&x)[VecOf<T>::value], float* pa
   }
 }
 
-template <typename T, int LPR, int NM, bool FAR, bool PRO>
-__global__ __launch_bounds__(kWalkBlock) void bwd_walk(Params p, WalkCfg c) {
-  constexpr int VEC = VecOf<T>::value;
-  const int64_t wave = wave_id();
-  int b, hg, a;
-  const bool live = decode_tile(p, c, wave, b, hg, a);
-  const int lane = threadIdx.x & 63;
-  BwdWalker<T, LPR, NM, FAR, PRO> w;
-  w.ln.zero(w.dwq);
-  w.ln.zero(w.dwk);
-  if (live) {
-    const int h = hg * (64 / LPR) + lane / LPR;
-    w.ln.init(p, lane % LPR);
-    auto rows = [&](const View& vw) {
-      return Rows<T>{reinterpret_cast<const T*>(vw.p) + (int64_t)b * vw.sb + (int64_t)h * vw.sh, vw.st};
-    };
-    w.q = rows(p.q);
-    w.k = rows(p.k);
-    w.v = rows(p.v);
-    w.go = rows(p.dout);
-    w.dq = reinterpret_cast<T*>(p.dq.p) + (int64_t)b * p.dq.sb + (int64_t)h * p.dq.sh;
-    w.dk = reinterpret_cast<T*>(p.dk.p) + (int64_t)b * p.dk.sb + (int64_t)h * p.dk.sh;
-    w.dv = reinterpret_cast<T*>(p.dv.p) + (int64_t)b * p.dv.sb + (int64_t)h * p.dv.sh;
-    w.dqst = p.dq.st;
-    w.dkst = p.dk.st;
-    w.dvst = p.dv.st;
-    w.lse = p.lse + (int64_t)b * p.T * p.H + h;
-  w.lst = p.H;
-    w.scale = p.scale;
-    w.F = c.F;
-    w.T_ = p.T;
-    w.a = a;
-    w.end = min(a + c.P, p.T);
-    w.qend = min(w.end + 2, p.T);
-    // Walk u = a-2 .. end+1; rotation slot of u is (u - a + 2) mod 3.
-    const int last = w.end + 1;
-    int u = a - 2;
-    for (; u + 3 <= last + 1; u += 3) {
-      w.template step<0>(u);
-      w.template step<1>(u + 1);
-      w.template step<2>(u + 2);
-    }
-    if (u <= last) w.template step<0>(u);
-    if (u + 1 <= last) w.template step<1>(u + 1);
-  }
-  if constexpr (PRO) {
-    write_wave_partial<T, LPR, true>(w.dwq, p.dwq_part, wave, p.D);
-    write_wave_partial<T, LPR, true>(w.dwk, p.dwk_part, wave, p.D);
-  }
-  (void)VEC;
-}
-
 // ========================================================= pipelined walks
 //
-// The same walks without the prologue, software-pipelined: while step u is
-// computed, every row step u+1 needs is already in flight.  Loads are
+// Software-pipelined walks (no prologue): while step u is computed, every
+// row step u+1 needs is already in flight.  Loads are
 // unconditional (positions clamped into [0, T), validity applied as masks)
 // so the compiler can keep them outstanding across steps.  Rows stay in
 // their 16-byte raw form; dot products use v_dot2_f32_{bf16,f16} on the raw
@@ -558,11 +146,12 @@ struct Raw {
   uint32_t w[4];
 };
 
-template <typename T>
-__device__ inline Raw load_raw(const T* __restrict__ row, int li) {
-  const uint4 x = *reinterpret_cast<const uint4*>(row + li * VecOf<T>::value);
-  return Raw{{x.x, x.y, x.z, x.w}};
-}
+// Cache policy.  Results are written with non-temporal stores (nothing
+// re-reads them in the kernel).  A row a wave loads for its own position is
+// re-read by no other wave when the pattern has no far offset, so those loads
+// are non-temporal too; with a far offset the neighbouring wave (column t + F)
+// reads the same rows, and they must stay in L2 / the Infinity Cache.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <typename T>
 __device__ inline void widen(const Raw& r, float (&x)[VecOf<T>::value]) {
@@ -593,19 +182,89 @@ __device__ inline float dot_raw(const Raw& a, const Raw& b) {
 
 __device__ inline int clampi(int x, int hi) { return x < 0 ? 0 : (x > hi ? hi : x); }
 
+// One tensor as a walking wave sees it: a wave-uniform base (batch and head
+// group applied) and row stride in bytes, plus this lane's byte offset inside
+// a position (its head within the group and its 16-byte chunk).  A load adds
+// the row's 32-bit byte offset (one scalar multiply per row) to the lane
+// offset (one full-rate vector add) and uses the scalar-base + 32-bit
+// vector-offset addressing form, so no per-lane 64-bit arithmetic is left in
+// the loop.  The host only picks these kernels when every offset of a head
+// group's span fits in 32 bits (walk_applies).
+struct Stream {
+  const char* base;
+  uint32_t st;
+  uint32_t lane;
+
+  __device__ inline uint32_t at(int t) const { return lane + (uint32_t)t * st; }
+};
+
+template <typename Vw>
+__device__ inline Stream make_stream(const Vw& vw, int esz, int b, int h0, int hl, int li) {
+  Stream s;
+  s.base = (const char*)vw.p + ((int64_t)b * vw.sb + (int64_t)h0 * vw.sh) * esz;
+  s.st = (uint32_t)(vw.st * esz);
+  s.lane = (uint32_t)((int64_t)hl * vw.sh * esz) + (uint32_t)li * 16u;
+  return s;
+}
+
+template <bool NT = false>
+__device__ inline Raw load_at(const Stream& s, int t) {
+  const u32x4* p = reinterpret_cast<const u32x4*>(s.base + (uint64_t)s.at(t));
+  u32x4 x;
+  if constexpr (NT) x = __builtin_nontemporal_load(p);
+  else x = *p;
+  return Raw{{x.x, x.y, x.z, x.w}};
+}
+
+template <typename T>
+__device__ inline void store_at(const Stream& s, int t, const float (&x)[VecOf<T>::value]) {
+  uint32_t w[4];
+  pack_words<T, 4>(x, w);
+  u32x4 v = {w[0], w[1], w[2], w[3]};
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(const_cast<char*>(s.base) + (uint64_t)s.at(t)));
+}
+
+__device__ inline float load_f32(const Stream& s, int t) {
+  return *reinterpret_cast<const float*>(s.base + (uint64_t)s.at(t));
+}
+
+__device__ inline void store_f32(const Stream& s, int t, float x) {
+  *reinterpret_cast<float*>(const_cast<char*>(s.base) + (uint64_t)s.at(t)) = x;
+}
+
+// lse rows: fp32 [B, T, H]; the group's heads are contiguous.
+__device__ inline Stream lse_stream(const Params& p, int b, int h0, int hl) {
+  Stream s;
+  s.base = (const char*)(p.lse + ((int64_t)b * p.T * p.H + h0));
+  s.st = (uint32_t)p.H * 4u;
+  s.lane = (uint32_t)hl * 4u;
+  return s;
+}
+
+// Wave-uniform tile decode shared by the pipelined walks.
+struct WaveTile {
+  int b, hg, a;
+  int hl, li;   // this lane's head within the group, 16-byte chunk within the row
+};
+
+template <int LPR>
+__device__ inline bool wave_tile(const Params& p, const WalkCfg& c, WaveTile& w) {
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int64_t n = xcd_remap(blockIdx.x, gridDim.x) * kWaves + wv;
+  if (!decode_tile(p, c, n, w.b, w.hg, w.a)) return false;
+  const int lane = threadIdx.x & 63;
+  w.hl = lane / LPR;
+  w.li = lane % LPR;
+  return true;
+}
+
 template <typename T, int LPR, int NM, bool FAR>
 struct FwdPipe {
   static constexpr int VEC = VecOf<T>::value;
   static constexpr int NN = NearSet<NM>::count;
   static constexpr int NS = NN + (FAR ? 1 : 0);
 
-  const T* __restrict__ q;
-  const T* __restrict__ k;
-  const T* __restrict__ v;
-  T* __restrict__ o;
-  float* __restrict__ lse;
-  int lst;
-  int64_t qst, kst, vst, ost;
+  Stream q, k, v, o, lse;
   float scale;
   int F, Tm1, li;
   Raw kr[4];            // k at t (slot R), t-1, t-2; slot R+1 is being fetched
@@ -616,13 +275,13 @@ struct FwdPipe {
   template <int R>
   __device__ inline void prefetch(int t) {
     const int tc = clampi(t, Tm1);
-    kr[R] = load_raw<T>(k + (int64_t)tc * kst, li);
-    vraw[R & 1] = load_raw<T>(v + (int64_t)tc * vst, li);
-    qn[R & 1] = load_raw<T>(q + (int64_t)tc * qst, li);
+    kr[R] = load_at<!FAR>(k, tc);
+    vraw[R & 1] = load_at<!FAR>(v, tc);
+    qn[R & 1] = load_at<!FAR>(q, tc);
     if constexpr (FAR) {
       const int tf = clampi(t - F, Tm1);
-      kl[R & 1] = load_raw<T>(k + (int64_t)tf * kst, li);
-      vl[R & 1] = load_raw<T>(v + (int64_t)tf * vst, li);
+      kl[R & 1] = load_at(k, tf);
+      vl[R & 1] = load_at(v, tf);
     }
   }
 
@@ -676,34 +335,29 @@ struct FwdPipe {
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[e] *= inv;
     if (store) {
-      store_row<T, false>(o + (int64_t)t * ost, li, VEC * LPR, acc);
-      if (li == 0) lse[(int64_t)t * lst] = l > 0.f ? m + fast_log(l) : INFINITY;
+      store_at<T>(o, t, acc);
+      if (li == 0) store_f32(lse, t, l > 0.f ? m + fast_log(l) : INFINITY);
     }
   }
 };
 
 template <typename T, int LPR, int NM, bool FAR>
 __global__ __launch_bounds__(kWalkBlock) void fwd_pipe(Params p, WalkCfg c) {
-  int b, hg, a;
-  if (!decode_tile(p, c, wave_id(), b, hg, a)) return;
-  const int lane = threadIdx.x & 63;
-  const int h = hg * (64 / LPR) + lane / LPR;
+  WaveTile wt;
+  if (!wave_tile<LPR>(p, c, wt)) return;
+  constexpr int G = 64 / LPR, esz = (int)sizeof(T);
+  const int h0 = wt.hg * G;
   FwdPipe<T, LPR, NM, FAR> w;
-  w.li = lane % LPR;
-  w.q = reinterpret_cast<const T*>(p.q.p) + (int64_t)b * p.q.sb + (int64_t)h * p.q.sh;
-  w.k = reinterpret_cast<const T*>(p.k.p) + (int64_t)b * p.k.sb + (int64_t)h * p.k.sh;
-  w.v = reinterpret_cast<const T*>(p.v.p) + (int64_t)b * p.v.sb + (int64_t)h * p.v.sh;
-  w.o = reinterpret_cast<T*>(p.o.p) + (int64_t)b * p.o.sb + (int64_t)h * p.o.sh;
-  w.qst = p.q.st;
-  w.kst = p.k.st;
-  w.vst = p.v.st;
-  w.ost = p.o.st;
-  w.lse = p.lse + (int64_t)b * p.T * p.H + h;
-  w.lst = p.H;
+  w.q = make_stream(p.q, esz, wt.b, h0, wt.hl, wt.li);
+  w.k = make_stream(p.k, esz, wt.b, h0, wt.hl, wt.li);
+  w.v = make_stream(p.v, esz, wt.b, h0, wt.hl, wt.li);
+  w.o = make_stream(p.o, esz, wt.b, h0, wt.hl, wt.li);
+  w.lse = lse_stream(p, wt.b, h0, wt.hl);
   w.scale = p.scale;
   w.F = c.F;
   w.Tm1 = p.T - 1;
-  const int end = min(a + c.P, p.T);
+  w.li = wt.li;
+  const int a = wt.a, end = min(a + c.P, p.T);
   // Slot of position t is (t - a + 2) & 3: the walk starts two positions
   // early (a-2, a-1) to fill the near-source rotation; those steps store nothing.
   const int t0 = a - 2;
@@ -726,18 +380,9 @@ struct BwdPipe {
   static constexpr int NN = NearSet<NM>::count;
   static constexpr int NS = NN + (FAR ? 1 : 0);
 
-  const T* __restrict__ q;
-  const T* __restrict__ k;
-  const T* __restrict__ v;
-  const T* __restrict__ go;
-  T* __restrict__ dq;
-  T* __restrict__ dk;
-  T* __restrict__ dv;
-  const float* __restrict__ lse;
-  int lst;
-  int64_t qst, kst, vst, gst, dqst, dkst, dvst;
+  Stream q, k, v, go, dq, dk, dv, lse;
   float scale;
-  int F, T_, Tm1, a, end, li;
+  int F, T_, Tm1, a, end;
   Raw kr[4], vr[4];     // own k/v rotation: slot of u is R
   Raw qr[4], gr[4];     // own q/dO rotation (key finalisation reads u-2 .. u)
   float lr[4];
@@ -750,21 +395,21 @@ struct BwdPipe {
   template <int R>
   __device__ inline void prefetch(int u) {
     const int uc = clampi(u, Tm1);
-    kr[R] = load_raw<T>(k + (int64_t)uc * kst, li);
-    vr[R] = load_raw<T>(v + (int64_t)uc * vst, li);
-    qr[R] = load_raw<T>(q + (int64_t)uc * qst, li);
-    gr[R] = load_raw<T>(go + (int64_t)uc * gst, li);
-    lr[R] = lse[(int64_t)uc * lst];
+    kr[R] = load_at<!FAR>(k, uc);
+    vr[R] = load_at<!FAR>(v, uc);
+    qr[R] = load_at<!FAR>(q, uc);
+    gr[R] = load_at<!FAR>(go, uc);
+    lr[R] = load_f32(lse, uc);
     if constexpr (FAR) {
       const int ul = clampi(u - F, Tm1);
-      kl[R & 1] = load_raw<T>(k + (int64_t)ul * kst, li);
-      vl[R & 1] = load_raw<T>(v + (int64_t)ul * vst, li);
+      kl[R & 1] = load_at(k, ul);
+      vl[R & 1] = load_at(v, ul);
       const int i = clampi(u - 2 + F, Tm1);
-      fk[R] = load_raw<T>(k + (int64_t)i * kst, li);
-      fv[R] = load_raw<T>(v + (int64_t)i * vst, li);
-      qi[R & 1] = load_raw<T>(q + (int64_t)i * qst, li);
-      gi[R & 1] = load_raw<T>(go + (int64_t)i * gst, li);
-      li_[R & 1] = lse[(int64_t)i * lst];
+      fk[R] = load_at(k, i);
+      fv[R] = load_at(v, i);
+      qi[R & 1] = load_at(q, i);
+      gi[R & 1] = load_at(go, i);
+      li_[R & 1] = load_f32(lse, i);
     }
   }
 
@@ -827,7 +472,7 @@ struct BwdPipe {
 #pragma unroll
           for (int e = 0; e < VEC; ++e) g[e] = __builtin_fmaf(c, kx[e], g[e]);
         }
-        store_row<T, false>(dq + (int64_t)u * dqst, li, VEC * LPR, g);
+        store_at<T>(dq, u, g);
       }
     }
     // Key j = u - 2: near contributions from queries j + n, far from j + F.
@@ -886,50 +531,35 @@ struct BwdPipe {
           av[e] = __builtin_fmaf(cp, gx[e], av[e]);
         }
       }
-      store_row<T, false>(dk + (int64_t)j * dkst, li, VEC * LPR, ak);
-      store_row<T, false>(dv + (int64_t)j * dvst, li, VEC * LPR, av);
+      store_at<T>(dk, j, ak);
+      store_at<T>(dv, j, av);
     }
   }
 };
 
 template <typename T, int LPR, int NM, bool FAR>
 __global__ __launch_bounds__(kWalkBlock) void bwd_pipe(Params p, WalkCfg c) {
-  int b, hg, a;
-  if (!decode_tile(p, c, wave_id(), b, hg, a)) return;
-  const int lane = threadIdx.x & 63;
-  const int h = hg * (64 / LPR) + lane / LPR;
+  WaveTile wt;
+  if (!wave_tile<LPR>(p, c, wt)) return;
+  constexpr int G = 64 / LPR, esz = (int)sizeof(T);
+  const int h0 = wt.hg * G;
   BwdPipe<T, LPR, NM, FAR> w;
-  w.li = lane % LPR;
-  auto base = [&](const View& vw) {
-    return reinterpret_cast<const T*>(vw.p) + (int64_t)b * vw.sb + (int64_t)h * vw.sh;
-  };
-  auto mbase = [&](const MutView& vw) {
-    return reinterpret_cast<T*>(vw.p) + (int64_t)b * vw.sb + (int64_t)h * vw.sh;
-  };
-  w.q = base(p.q);
-  w.k = base(p.k);
-  w.v = base(p.v);
-  w.go = base(p.dout);
-  w.dq = mbase(p.dq);
-  w.dk = mbase(p.dk);
-  w.dv = mbase(p.dv);
-  w.qst = p.q.st;
-  w.kst = p.k.st;
-  w.vst = p.v.st;
-  w.gst = p.dout.st;
-  w.dqst = p.dq.st;
-  w.dkst = p.dk.st;
-  w.dvst = p.dv.st;
-  w.lse = p.lse + (int64_t)b * p.T * p.H + h;
-  w.lst = p.H;
+  w.q = make_stream(p.q, esz, wt.b, h0, wt.hl, wt.li);
+  w.k = make_stream(p.k, esz, wt.b, h0, wt.hl, wt.li);
+  w.v = make_stream(p.v, esz, wt.b, h0, wt.hl, wt.li);
+  w.go = make_stream(p.dout, esz, wt.b, h0, wt.hl, wt.li);
+  w.dq = make_stream(p.dq, esz, wt.b, h0, wt.hl, wt.li);
+  w.dk = make_stream(p.dk, esz, wt.b, h0, wt.hl, wt.li);
+  w.dv = make_stream(p.dv, esz, wt.b, h0, wt.hl, wt.li);
+  w.lse = lse_stream(p, wt.b, h0, wt.hl);
   w.scale = p.scale;
   w.F = c.F;
   w.T_ = p.T;
   w.Tm1 = p.T - 1;
-  w.a = a;
-  w.end = min(a + c.P, p.T);
+  w.a = wt.a;
+  w.end = min(wt.a + c.P, p.T);
   // Walk u = a-2 .. end+1 (slot of u is (u - a + 2) & 3).
-  const int u0 = a - 2, last = w.end + 1;
+  const int u0 = wt.a - 2, last = w.end + 1;
   w.template prefetch<0>(u0);
   for (int u = u0; u <= last; u += 4) {
     w.template prefetch<1>(u + 1);
@@ -940,6 +570,304 @@ __global__ __launch_bounds__(kWalkBlock) void bwd_pipe(Params p, WalkCfg c) {
     w.template compute<2>(u + 2);
     w.template prefetch<0>(u + 4);
     w.template compute<3>(u + 3);
+  }
+}
+
+// ============================================== chained backward (far >= tile)
+//
+// With the far offset F a multiple of the tile P, the tiles of one band form
+// a column t, t + F, t + 2F, ...: the far-left sources of row r + 1 are row
+// r's own k/v rows, and the far query of row r's key j is row r + 1's query
+// j + F.  Independent waves re-read those rows from L2 a few steps after
+// their owner loaded them, and at the streaming rate of a whole XCD most of
+// them have been evicted by then.  Here a workgroup of W waves walks W
+// consecutive rows of one band in lockstep (one barrier per step) and passes
+// the rows through LDS instead: wave w publishes its k/v (for wave w + 1's
+// far-left slot) and its q/dO plus the far slot's (p, scale dS) (for wave
+// w - 1's far key contribution).  Only the first wave loads far-left rows
+// and only the last wave recomputes its far queries from global memory.
+//
+// Every wave of the workgroup runs the same number of steps (tiles past the
+// end of the sequence walk clamped rows and store nothing), so all barriers
+// are reached by all waves.
+
+constexpr int kChainRing = 4;   // q/dO/weight ring: written at step u, read at u + 2
+
+struct ChainSlot {
+  u32x4 kv[2][2][64];             // [u & 1][k, v][lane]
+  u32x4 qd[kChainRing][2][64];    // [u & 3][q, dO][lane]
+  float2 pd[kChainRing][64];      // [u & 3][lane]: (p_far, scale * dS_far) of query u
+};
+
+struct ChainCfg {
+  int P, F, rows, W, bands, blocks;   // blocks: row blocks (ceil(rows / W)) per band
+  int HG, nwg;
+};
+
+template <typename T, int LPR, int NM, bool LEFT_LDS, bool RIGHT_LDS>
+struct BwdChain {
+  static constexpr int VEC = VecOf<T>::value;
+  static constexpr int NN = NearSet<NM>::count;
+  static constexpr int NS = NN + 1;
+
+  Stream q, k, v, go, dq, dk, dv, lse;
+  float scale;
+  int F, T_, Tm1, a, end, lane;
+  ChainSlot* mine;
+  const ChainSlot* up;     // wave w - 1 (far-left provider)
+  const ChainSlot* down;   // wave w + 1 (far-right provider)
+  Raw kr[4], vr[4], qr[4], gr[4];
+  float lr[4];
+  Raw fk[4], fv[4];        // far-right k/v rotation over i = u - 2 + F (last wave)
+  Raw kl[2], vl[2];        // far-left sources of query u (first wave)
+  Raw qi[2], gi[2];
+  float li_[2];
+  float sp[4][3], sd[4][3];
+
+  template <int R>
+  __device__ inline void prefetch(int u) {
+    const int uc = clampi(u, Tm1);
+    kr[R] = load_at(k, uc);
+    vr[R] = load_at(v, uc);
+    qr[R] = load_at(q, uc);
+    gr[R] = load_at(go, uc);
+    lr[R] = load_f32(lse, uc);
+    if constexpr (!LEFT_LDS) {
+      const int ul = clampi(u - F, Tm1);
+      kl[R & 1] = load_at(k, ul);
+      vl[R & 1] = load_at(v, ul);
+    }
+    if constexpr (!RIGHT_LDS) {
+      const int i = clampi(u - 2 + F, Tm1);
+      fk[R] = load_at(k, i);
+      fv[R] = load_at(v, i);
+      qi[R & 1] = load_at(q, i);
+      gi[R & 1] = load_at(go, i);
+      li_[R & 1] = load_f32(lse, i);
+    }
+  }
+
+  __device__ static inline u32x4 pack(const Raw& r) { return u32x4{r.w[0], r.w[1], r.w[2], r.w[3]}; }
+  __device__ static inline Raw unpack(const u32x4& x) { return Raw{{x.x, x.y, x.z, x.w}}; }
+
+  __device__ inline void grads(const Raw& qq, const Raw& gg, float l, const Raw* const (&ks)[NS],
+                               const Raw* const (&vs)[NS], const bool (&ok)[NS], float (&pp)[NS],
+                               float (&ds)[NS]) const {
+    float dp[NS];
+    float delta = 0.f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const float sc = row_sum<LPR>(dot_raw<T>(qq, *ks[s])) * scale;
+      dp[s] = row_sum<LPR>(dot_raw<T>(gg, *vs[s]));
+      pp[s] = ok[s] ? fast_exp(sc - l) : 0.f;
+      delta = __builtin_fmaf(pp[s], dp[s], delta);
+    }
+#pragma unroll
+    for (int s = 0; s < NS; ++s) ds[s] = pp[s] * (dp[s] - delta);
+  }
+
+  template <int R>
+  __device__ inline void compute(int u) {
+    // Publish this step's rows, then wait for the neighbours' rows.
+    mine->kv[R & 1][0][lane] = pack(kr[R]);
+    mine->kv[R & 1][1][lane] = pack(vr[R]);
+    mine->qd[R][0][lane] = pack(qr[R]);
+    mine->qd[R][1][lane] = pack(gr[R]);
+    __syncthreads();
+    Raw kf, vf;
+    if constexpr (LEFT_LDS) {
+      kf = unpack(up->kv[R & 1][0][lane]);
+      vf = unpack(up->kv[R & 1][1][lane]);
+    } else {
+      kf = kl[R & 1];
+      vf = vl[R & 1];
+    }
+    {
+      const Raw* ks[NS];
+      const Raw* vs[NS];
+      bool ok[NS];
+      int idx = 0;
+#pragma unroll
+      for (int n = 0; n < 3; ++n) {
+        if (NM & (1 << n)) {
+          ks[idx] = &kr[(R + 4 - n) & 3];
+          vs[idx] = &vr[(R + 4 - n) & 3];
+          ok[idx] = u - n >= 0;
+          ++idx;
+        }
+      }
+      ks[NS - 1] = &kf;
+      vs[NS - 1] = &vf;
+      ok[NS - 1] = u - F >= 0;
+      float pp[NS], ds[NS];
+      grads(qr[R], gr[R], lr[R], ks, vs, ok, pp, ds);
+#pragma unroll
+      for (int n = 0; n < NN; ++n) {
+        sp[R][n] = pp[n];
+        sd[R][n] = ds[n] * scale;
+      }
+      mine->pd[R][lane] = make_float2(pp[NS - 1], ds[NS - 1] * scale);
+      if (u >= a && u < end) {
+        float g[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) g[e] = 0.f;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          float kx[VEC];
+          widen<T>(*ks[s], kx);
+          const float c = ds[s] * scale;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) g[e] = __builtin_fmaf(c, kx[e], g[e]);
+        }
+        store_at<T>(dq, u, g);
+      }
+    }
+    // Key j = u - 2: near contributions from queries j + n, far from j + F.
+    const int j = u - 2;
+    if (j >= a && j < end) {
+      float ak[VEC], av[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) { ak[e] = 0.f; av[e] = 0.f; }
+      int idx = 0;
+#pragma unroll
+      for (int n = 0; n < 3; ++n) {
+        if (NM & (1 << n)) {
+          const int slot = (R + 2 + n) & 3;
+          const bool there = j + n < T_;
+          const float cs = there ? sd[slot][idx] : 0.f;
+          const float cp = there ? sp[slot][idx] : 0.f;
+          float qx[VEC], gx[VEC];
+          widen<T>(qr[slot], qx);
+          widen<T>(gr[slot], gx);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            ak[e] = __builtin_fmaf(cs, qx[e], ak[e]);
+            av[e] = __builtin_fmaf(cp, gx[e], av[e]);
+          }
+          ++idx;
+        }
+      }
+      const bool there = j + F < T_;
+      float cs, cp;
+      Raw qf, gf;
+      if constexpr (RIGHT_LDS) {
+        // Query j + F is wave w + 1's query of step u - 2.
+        const float2 w2 = down->pd[(R + 2) & 3][lane];
+        qf = unpack(down->qd[(R + 2) & 3][0][lane]);
+        gf = unpack(down->qd[(R + 2) & 3][1][lane]);
+        cs = there ? w2.y : 0.f;
+        cp = there ? w2.x : 0.f;
+      } else {
+        const Raw* ks[NS];
+        const Raw* vs[NS];
+        bool ok[NS];
+        int n2 = 0;
+#pragma unroll
+        for (int n = 0; n < 3; ++n) {
+          if (NM & (1 << n)) {
+            ks[n2] = &fk[(R + 4 - n) & 3];
+            vs[n2] = &fv[(R + 4 - n) & 3];
+            ok[n2] = true;   // i - n >= F - 2 > 0
+            ++n2;
+          }
+        }
+        ks[NS - 1] = &kr[(R + 2) & 3];
+        vs[NS - 1] = &vr[(R + 2) & 3];
+        ok[NS - 1] = true;
+        float pp[NS], ds[NS];
+        grads(qi[R & 1], gi[R & 1], li_[R & 1], ks, vs, ok, pp, ds);
+        qf = qi[R & 1];
+        gf = gi[R & 1];
+        cs = there ? ds[NS - 1] * scale : 0.f;
+        cp = there ? pp[NS - 1] : 0.f;
+      }
+      float qx[VEC], gx[VEC];
+      widen<T>(qf, qx);
+      widen<T>(gf, gx);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        ak[e] = __builtin_fmaf(cs, qx[e], ak[e]);
+        av[e] = __builtin_fmaf(cp, gx[e], av[e]);
+      }
+      store_at<T>(dk, j, ak);
+      store_at<T>(dv, j, av);
+    }
+  }
+
+  __device__ inline void walk(int steps_from) {
+    // u = a-2 .. a+P+1 for every wave of the workgroup (same trip count).
+    const int u0 = steps_from;
+    prefetch<0>(u0);
+    for (int u = u0; u <= u0 + (end_u - u0); u += 4) {
+      prefetch<1>(u + 1);
+      compute<0>(u);
+      prefetch<2>(u + 2);
+      compute<1>(u + 1);
+      prefetch<3>(u + 3);
+      compute<2>(u + 2);
+      prefetch<0>(u + 4);
+      compute<3>(u + 3);
+    }
+  }
+  int end_u;
+};
+
+template <typename T, int LPR, int NM, bool LEFT_LDS, bool RIGHT_LDS>
+__device__ inline void chain_wave(const Params& p, const ChainCfg& c, ChainSlot* lds, int w, int b,
+                                  int h0, int a, int hl, int li) {
+  constexpr int esz = (int)sizeof(T);
+  BwdChain<T, LPR, NM, LEFT_LDS, RIGHT_LDS> x;
+  x.q = make_stream(p.q, esz, b, h0, hl, li);
+  x.k = make_stream(p.k, esz, b, h0, hl, li);
+  x.v = make_stream(p.v, esz, b, h0, hl, li);
+  x.go = make_stream(p.dout, esz, b, h0, hl, li);
+  x.dq = make_stream(p.dq, esz, b, h0, hl, li);
+  x.dk = make_stream(p.dk, esz, b, h0, hl, li);
+  x.dv = make_stream(p.dv, esz, b, h0, hl, li);
+  x.lse = lse_stream(p, b, h0, hl);
+  x.scale = p.scale;
+  x.F = c.F;
+  x.T_ = p.T;
+  x.Tm1 = p.T - 1;
+  x.a = a;
+  x.end = min(a + c.P, p.T);   // < a for a row past the end: nothing is stored
+  x.lane = threadIdx.x & 63;
+  x.mine = lds + w;
+  x.up = lds + (w > 0 ? w - 1 : 0);
+  x.down = lds + (w + 1 < c.W ? w + 1 : w);
+  // The trip count depends only on P: u = a-2 .. a+P+1 in steps of 4.
+  x.end_u = a + c.P + 1;
+  x.walk(a - 2);
+}
+
+template <typename T, int LPR, int NM, int W>
+__global__ __launch_bounds__(64 * W) void bwd_chain(Params p, ChainCfg c) {
+  __shared__ ChainSlot lds[W];
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  // Workgroup -> (batch, head group, band, row block), XCD-contiguous.
+  int64_t g = xcd_remap(blockIdx.x, gridDim.x);
+  const int rb = (int)(g % c.blocks);
+  g /= c.blocks;
+  const int cb = (int)(g % c.bands);
+  g /= c.bands;
+  const int hg = (int)(g % c.HG);
+  const int b = (int)(g / c.HG);
+  const int r = rb * W + w;
+  // Rows past the end (the last row block is padded to W rows) start at T:
+  // their loads are clamped and they store nothing.
+  const int64_t a64 = (int64_t)r * c.F + (int64_t)cb * c.P;
+  const int a = a64 < p.T ? (int)a64 : p.T;
+  const int lane = threadIdx.x & 63;
+  const int hl = lane / LPR, li = lane % LPR;
+  const int h0 = hg * (64 / LPR);
+  if (W == 1) {
+    chain_wave<T, LPR, NM, false, false>(p, c, lds, w, b, h0, a, hl, li);
+  } else if (w == 0) {
+    chain_wave<T, LPR, NM, false, true>(p, c, lds, w, b, h0, a, hl, li);
+  } else if (w == W - 1) {
+    chain_wave<T, LPR, NM, true, false>(p, c, lds, w, b, h0, a, hl, li);
+  } else {
+    chain_wave<T, LPR, NM, true, true>(p, c, lds, w, b, h0, a, hl, li);
   }
 }
 
@@ -958,12 +886,35 @@ __global__ __launch_bounds__(kWalkBlock) void bwd_pipe(Params p, WalkCfg c) {
 //     (far slot) using that table -- no weight recomputation -- then dK
 //     through the transposed prologue.
 
-template <typename T>
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <typename T, bool NT = false>
 __device__ inline Raw load_raw_split(const T* __restrict__ row, int li, int D) {
   constexpr int HV = VecOf<T>::value / 2;
-  const uint2 x = *reinterpret_cast<const uint2*>(row + li * HV);
-  const uint2 y = *reinterpret_cast<const uint2*>(row + (D >> 1) + li * HV);
+  const u32x2* px = reinterpret_cast<const u32x2*>(row + li * HV);
+  const u32x2* py = reinterpret_cast<const u32x2*>(row + (D >> 1) + li * HV);
+  u32x2 x, y;
+  if constexpr (NT) {
+    x = __builtin_nontemporal_load(px);
+    y = __builtin_nontemporal_load(py);
+  } else {
+    x = *px;
+    y = *py;
+  }
   return Raw{{x.x, x.y, y.x, y.y}};
+}
+
+// Split-layout counterpart of store_raw (two 8-byte non-temporal stores).
+template <typename T>
+__device__ inline void store_split_nt(T* __restrict__ row, int li, int D,
+                                      const float (&x)[VecOf<T>::value]) {
+  constexpr int HV = VecOf<T>::value / 2;
+  uint32_t wa[2], wb[2];
+  pack_words<T, 2>(x, wa);
+  pack_words<T, 2>(x + HV, wb);
+  __builtin_nontemporal_store(u32x2{wa[0], wa[1]}, reinterpret_cast<u32x2*>(row + li * HV));
+  __builtin_nontemporal_store(u32x2{wb[0], wb[1]},
+                              reinterpret_cast<u32x2*>(row + (D >> 1) + li * HV));
 }
 
 template <typename T, int LPR>
@@ -1021,9 +972,9 @@ struct FwdPipePro : ProBase<T, LPR> {
   template <int R>
   __device__ inline void prefetch(int t) {
     const int tc = clampi(t, this->Tm1);
-    kraw[R & 1] = load_raw_split<T>(k + (int64_t)tc * kst, this->li, this->D);
-    qraw[R & 1] = load_raw_split<T>(q + (int64_t)tc * qst, this->li, this->D);
-    vraw[R & 1] = load_raw_split<T>(v + (int64_t)tc * vst, this->li, this->D);
+    kraw[R & 1] = load_raw_split<T, !FAR>(k + (int64_t)tc * kst, this->li, this->D);
+    qraw[R & 1] = load_raw_split<T, !FAR>(q + (int64_t)tc * qst, this->li, this->D);
+    vraw[R & 1] = load_raw_split<T, !FAR>(v + (int64_t)tc * vst, this->li, this->D);
     this->cs(tc, cc[R & 1], ss[R & 1]);
     if constexpr (FAR) {
       const int tf = clampi(t - F, this->Tm1);
@@ -1088,7 +1039,7 @@ struct FwdPipePro : ProBase<T, LPR> {
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[e] *= inv;
     if (store) {
-      store_row<T, true>(o + (int64_t)t * ost, this->li, this->D, acc);
+      store_split_nt<T>(o + (int64_t)t * ost, this->li, this->D, acc);
       if (this->li == 0) lse[(int64_t)t * lst] = l > 0.f ? m + fast_log(l) : INFINITY;
     }
   }
@@ -1160,10 +1111,10 @@ struct BwdQPro : ProBase<T, LPR> {
   template <int R>
   __device__ inline void prefetch(int u) {
     const int uc = clampi(u, this->Tm1);
-    kraw[R & 1] = load_raw_split<T>(k + (int64_t)uc * kst, this->li, this->D);
-    vr[R] = load_raw_split<T>(v + (int64_t)uc * vst, this->li, this->D);
-    qraw[R & 1] = load_raw_split<T>(q + (int64_t)uc * qst, this->li, this->D);
-    graw[R & 1] = load_raw_split<T>(go + (int64_t)uc * gst, this->li, this->D);
+    kraw[R & 1] = load_raw_split<T, !FAR>(k + (int64_t)uc * kst, this->li, this->D);
+    vr[R] = load_raw_split<T, !FAR>(v + (int64_t)uc * vst, this->li, this->D);
+    qraw[R & 1] = load_raw_split<T, !FAR>(q + (int64_t)uc * qst, this->li, this->D);
+    graw[R & 1] = load_raw_split<T, !FAR>(go + (int64_t)uc * gst, this->li, this->D);
     lv[R & 1] = lse[(int64_t)uc * lst];
     this->cs(uc, cc[R & 1], ss[R & 1]);
     if constexpr (FAR) {
@@ -1224,7 +1175,7 @@ struct BwdQPro : ProBase<T, LPR> {
         for (int e = 0; e < VEC; ++e) g[e] = __builtin_fmaf(ds[s], ks[s][e], g[e]);
       }
       PL::backward_w(g, qx, rq, this->wq, cc[R & 1], ss[R & 1], this->D, dw);
-      store_row<T, true>(dq + (int64_t)u * dqst, this->li, this->D, g);
+      store_split_nt<T>(dq + (int64_t)u * dqst, this->li, this->D, g);
       float* trow = tab + (int64_t)u * tst;
 #pragma unroll
       for (int vix = 0; vix < 2 * NS; ++vix) {
@@ -1264,12 +1215,12 @@ struct BwdKPro : ProBase<T, LPR> {
   template <int R>
   __device__ inline void prefetch(int u) {
     const int uc = clampi(u, this->Tm1);
-    qraw[R & 1] = load_raw_split<T>(q + (int64_t)uc * qst, this->li, this->D);
-    gr[R] = load_raw_split<T>(go + (int64_t)uc * gst, this->li, this->D);
+    qraw[R & 1] = load_raw_split<T, !FAR>(q + (int64_t)uc * qst, this->li, this->D);
+    gr[R] = load_raw_split<T, !FAR>(go + (int64_t)uc * gst, this->li, this->D);
     this->cs(uc, cc[R & 1], ss[R & 1]);
     const int j = u - 2;
     const int jc = clampi(j, this->Tm1);
-    kraw[R & 1] = load_raw_split<T>(k + (int64_t)jc * kst, this->li, this->D);
+    kraw[R & 1] = load_raw_split<T, !FAR>(k + (int64_t)jc * kst, this->li, this->D);
     this->cs(jc, ckc[R & 1], cks[R & 1]);
     int idx = 0;
 #pragma unroll
@@ -1335,8 +1286,8 @@ struct BwdKPro : ProBase<T, LPR> {
       widen<T>(kraw[R & 1], kx);
       const float rk = PL::rms_factor(kx, this->D, this->eps);
       PL::backward_w(ak, kx, rk, this->wk, ckc[R & 1], cks[R & 1], this->D, dw);
-      store_row<T, true>(dk + (int64_t)j * dkst, this->li, this->D, ak);
-      store_row<T, true>(dv + (int64_t)j * dvst, this->li, this->D, av);
+      store_split_nt<T>(dk + (int64_t)j * dkst, this->li, this->D, ak);
+      store_split_nt<T>(dv + (int64_t)j * dvst, this->li, this->D, av);
     }
   }
 };
@@ -1479,11 +1430,11 @@ WalkCfg make_cfg(const Params& p, int lpr, const Pattern& pat) {
   // About 8192 tiles fill 256 CUs several times over; the tile is at least
   // 16 positions (halo overhead <= 2/16) and at most 256.
   int P = 256;
-  while (P > 16 && lanes_rows * ((p.T + P - 1) / P) < 8192) P >>= 1;
+  while (P > 16 && lanes_rows * ((p.T + P - 1) / P) < kWalkTiles) P >>= 1;
   // A far offset inside the tile would make a wave re-read rows it loaded F
   // steps earlier, long evicted from L2.  With the tile shrunk to F the far
-  // rows belong to the neighbouring tile, which a neighbouring wave walks at
-  // the same time, so they are L2 hits.
+  // rows belong to the neighbouring tile of the same column, which the
+  // backward's chained workgroups share through LDS.
   if (pat.far >= 16 && pat.far < P && (pat.far & (pat.far - 1)) == 0) P = pat.far;
   c.P = P;
   c.F = pat.far;
@@ -1501,15 +1452,41 @@ WalkCfg make_cfg(const Params& p, int lpr, const Pattern& pat) {
   return c;
 }
 
+template <typename T, int LPR, int NM>
+hipError_t launch_chain(const Params& p, const WalkCfg& wc, hipStream_t st) {
+  ChainCfg c{};
+  c.P = wc.P;
+  c.F = wc.F;
+  c.rows = wc.rows;
+  c.W = c.rows >= 8 ? 8 : c.rows >= 4 ? 4 : c.rows >= 2 ? 2 : 1;
+  c.bands = wc.F / wc.P;
+  c.blocks = (c.rows + c.W - 1) / c.W;
+  c.HG = wc.HG;
+  const int64_t nwg = (int64_t)p.B * c.HG * c.bands * c.blocks;
+  if (nwg <= 0 || nwg > 0x7fffffff) return hipErrorInvalidValue;
+  c.nwg = (int)nwg;
+  const dim3 grid((unsigned)c.nwg), block(64 * c.W);
+  switch (c.W) {
+    case 8: hipLaunchKernelGGL((bwd_chain<T, LPR, NM, 8>), grid, block, 0, st, p, c); break;
+    case 4: hipLaunchKernelGGL((bwd_chain<T, LPR, NM, 4>), grid, block, 0, st, p, c); break;
+    case 2: hipLaunchKernelGGL((bwd_chain<T, LPR, NM, 2>), grid, block, 0, st, p, c); break;
+    default: hipLaunchKernelGGL((bwd_chain<T, LPR, NM, 1>), grid, block, 0, st, p, c); break;
+  }
+  return hipGetLastError();
+}
+
 template <typename T, int LPR, bool PRO, bool FWD>
 hipError_t launch_pattern(const Params& p, const WalkCfg& c, const Pattern& pat, hipStream_t st) {
   const dim3 grid((unsigned)c.nwg), block(kWalkBlock);
+  if (!FWD && !PRO && pat.far != 0 && c.column) {
+    return pat.nm == 7 ? launch_chain<T, LPR, 7>(p, c, st) : launch_chain<T, LPR, 1>(p, c, st);
+  }
 #define SBDA_WALK_CASE(NMV, FARV)                                                            \
   if (pat.nm == NMV && (pat.far != 0) == FARV) {                                             \
     if (FWD && PRO) {                                                                        \
       hipLaunchKernelGGL((fwd_pipe_pro<T, LPR, NMV, FARV>), grid, block, 0, st, p, c);      \
     } else if (FWD) {                                                                        \
-      hipLaunchKernelGGL((fwd_pipe<T, LPR, NMV, FARV>), grid, block, 0, st, p, c);          \
+      hipLaunchKernelGGL((fwd_pipe<T, LPR, NMV, FARV>), grid, block, kFwdLdsCap, st, p, c);     \
     } else if (PRO) {                                                                        \
       hipLaunchKernelGGL((bwd_q_pro<T, LPR, NMV, FARV>), grid, block, 0, st, p, c);         \
       hipError_t e_ = hipGetLastError();                                                     \
@@ -1563,12 +1540,29 @@ hipError_t walk_launch(const Params& p, int dtype, bool pro, hipStream_t st) {
 
 }  // namespace
 
+// Every byte offset a wave forms from its head group's base (row offset plus
+// lane offset) must fit the 32-bit vector offset of the load/store form.
+template <typename Vw>
+bool span_fits_32(const Vw& vw, const Params& p, int esz, int lpr) {
+  if (vw.p == nullptr) return true;
+  if (vw.st < 0 || vw.sh < 0) return false;
+  const int64_t span =
+      ((int64_t)(p.T - 1) * vw.st + (int64_t)(64 / lpr - 1) * vw.sh) * esz + 16 * lpr;
+  return span <= (int64_t)0xffffffffLL;
+}
+
 bool walk_applies(const Params& p, int dtype) {
   Pattern pat;
   if (p.group != 1 || p.seg != nullptr || !classify(p, &pat)) return false;
   const int lpr = walk_lpr(p, dtype);
   if (lpr == 0) return false;
-  return p.H % (64 / lpr) == 0;
+  if (p.H % (64 / lpr) != 0) return false;
+  const int esz = dtype == kFP32 ? 4 : 2;
+  if ((int64_t)p.T * p.H * 4 > (int64_t)0xffffffffLL) return false;
+  return span_fits_32(p.q, p, esz, lpr) && span_fits_32(p.k, p, esz, lpr) &&
+         span_fits_32(p.v, p, esz, lpr) && span_fits_32(p.dout, p, esz, lpr) &&
+         span_fits_32(p.o, p, esz, lpr) && span_fits_32(p.dq, p, esz, lpr) &&
+         span_fits_32(p.dk, p, esz, lpr) && span_fits_32(p.dv, p, esz, lpr);
 }
 
 hipError_t walk_forward(const Params& p, int dtype, bool pro, hipStream_t st) {

@@ -258,19 +258,24 @@ __device__ inline bool wave_tile(const Params& p, const WalkCfg& c, WaveTile& w)
   return true;
 }
 
-template <typename T, int LPR, int NM, bool FAR>
+// FR > 0: the far offset is the compile-time constant FR (4 or 8) and the far
+// row is taken from the rotation (depth FR + 2) instead of being loaded: a
+// row loaded FR steps earlier is long gone from L2 at the streaming rate.
+template <typename T, int LPR, int NM, bool FAR, int FR>
 struct FwdPipe {
   static constexpr int VEC = VecOf<T>::value;
   static constexpr int NN = NearSet<NM>::count;
   static constexpr int NS = NN + (FAR ? 1 : 0);
+  static constexpr int RD = FR > 0 ? FR + 2 : 4;   // rotation depth (even)
+  static_assert(FR == 0 || FAR, "a rotation far source needs a far slot");
 
   Stream q, k, v, o, lse;
   float scale;
   int F, Tm1, li;
-  Raw kr[4];            // k at t (slot R), t-1, t-2; slot R+1 is being fetched
+  Raw kr[RD];           // k at t (slot R), t-1, ...; slot R+1 is being fetched
   Raw vraw[2], qn[2];   // this step's v and q (stage R & 1)
-  Raw kl[2], vl[2];     // far source t - F
-  float vr[4][VEC];     // widened v rotation
+  Raw kl[2], vl[2];     // far source t - F (FR == 0)
+  float vr[RD][VEC];    // widened v rotation
 
   template <int R>
   __device__ inline void prefetch(int t) {
@@ -278,7 +283,7 @@ struct FwdPipe {
     kr[R] = load_at<!FAR>(k, tc);
     vraw[R & 1] = load_at<!FAR>(v, tc);
     qn[R & 1] = load_at<!FAR>(q, tc);
-    if constexpr (FAR) {
+    if constexpr (FAR && FR == 0) {
       const int tf = clampi(t - F, Tm1);
       kl[R & 1] = load_at(k, tf);
       vl[R & 1] = load_at(v, tf);
@@ -295,15 +300,22 @@ struct FwdPipe {
     for (int n = 0; n < 3; ++n) {
       if (NM & (1 << n)) {
         ok[idx] = t - n >= 0;
-        sc[idx] = row_sum<LPR>(dot_raw<T>(qn[R & 1], kr[(R + 4 - n) & 3])) * scale;
+        sc[idx] = row_sum<LPR>(dot_raw<T>(qn[R & 1], kr[(R + RD - n) % RD])) * scale;
         ++idx;
       }
     }
     float vf[VEC];
     if constexpr (FAR) {
       ok[NS - 1] = t - F >= 0;
-      sc[NS - 1] = row_sum<LPR>(dot_raw<T>(qn[R & 1], kl[R & 1])) * scale;
-      widen<T>(vl[R & 1], vf);
+      if constexpr (FR > 0) {
+        constexpr int sf = (R + RD - FR) % RD;
+        sc[NS - 1] = row_sum<LPR>(dot_raw<T>(qn[R & 1], kr[sf])) * scale;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) vf[e] = vr[sf][e];
+      } else {
+        sc[NS - 1] = row_sum<LPR>(dot_raw<T>(qn[R & 1], kl[R & 1])) * scale;
+        widen<T>(vl[R & 1], vf);
+      }
     }
     float m = -INFINITY;
 #pragma unroll
@@ -321,7 +333,7 @@ struct FwdPipe {
 #pragma unroll
     for (int n = 0; n < 3; ++n) {
       if (NM & (1 << n)) {
-        const int slot = (R + 4 - n) & 3;
+        const int slot = (R + RD - n) % RD;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) acc[e] = __builtin_fmaf(w[idx], vr[slot][e], acc[e]);
         ++idx;
@@ -339,15 +351,26 @@ struct FwdPipe {
       if (li == 0) store_f32(lse, t, l > 0.f ? m + fast_log(l) : INFINITY);
     }
   }
+
+  // Steps R .. RD-1 of one trip around the rotation (position of slot 0 is t).
+  template <int R>
+  __device__ inline void steps(int t, int a, int end) {
+    if constexpr (R < RD) {
+      prefetch<(R + 1) % RD>(t + R + 1);
+      compute<R>(t + R, t + R >= a && t + R < end);
+      steps<R + 1>(t, a, end);
+    }
+  }
 };
 
-template <typename T, int LPR, int NM, bool FAR>
+template <typename T, int LPR, int NM, bool FAR, int FR>
 __global__ __launch_bounds__(kWalkBlock) void fwd_pipe(Params p, WalkCfg c) {
   WaveTile wt;
   if (!wave_tile<LPR>(p, c, wt)) return;
   constexpr int G = 64 / LPR, esz = (int)sizeof(T);
   const int h0 = wt.hg * G;
-  FwdPipe<T, LPR, NM, FAR> w;
+  using W = FwdPipe<T, LPR, NM, FAR, FR>;
+  W w;
   w.q = make_stream(p.q, esz, wt.b, h0, wt.hl, wt.li);
   w.k = make_stream(p.k, esz, wt.b, h0, wt.hl, wt.li);
   w.v = make_stream(p.v, esz, wt.b, h0, wt.hl, wt.li);
@@ -358,20 +381,12 @@ __global__ __launch_bounds__(kWalkBlock) void fwd_pipe(Params p, WalkCfg c) {
   w.Tm1 = p.T - 1;
   w.li = wt.li;
   const int a = wt.a, end = min(a + c.P, p.T);
-  // Slot of position t is (t - a + 2) & 3: the walk starts two positions
-  // early (a-2, a-1) to fill the near-source rotation; those steps store nothing.
-  const int t0 = a - 2;
+  // The walk starts early enough to fill the rotation (2 positions, or FR
+  // for a rotation far source); those steps store nothing.  Slot of
+  // position t is (t - t0) % RD.
+  const int t0 = a - (FR > 2 ? FR : 2);
   w.template prefetch<0>(t0);
-  for (int t = t0; t < end; t += 4) {
-    w.template prefetch<1>(t + 1);
-    w.template compute<0>(t, t >= a && t < end);
-    w.template prefetch<2>(t + 2);
-    w.template compute<1>(t + 1, t + 1 >= a && t + 1 < end);
-    w.template prefetch<3>(t + 3);
-    w.template compute<2>(t + 2, t + 2 >= a && t + 2 < end);
-    w.template prefetch<0>(t + 4);
-    w.template compute<3>(t + 3, t + 3 >= a && t + 3 < end);
-  }
+  for (int t = t0; t < end; t += W::RD) w.template steps<0>(t, a, end);
 }
 
 template <typename T, int LPR, int NM, bool FAR>
@@ -868,6 +883,261 @@ __global__ __launch_bounds__(64 * W) void bwd_chain(Params p, ChainCfg c) {
     chain_wave<T, LPR, NM, true, false>(p, c, lds, w, b, h0, a, hl, li);
   } else {
     chain_wave<T, LPR, NM, true, true>(p, c, lds, w, b, h0, a, hl, li);
+  }
+}
+
+// ============================================= transposed chain (far = 4, 8)
+//
+// For a small far offset F the far rows are F steps back in a wave's own walk
+// -- evicted from L2 by then.  Here the sequence is seen as rows of F
+// positions (t = r * F + c) and a workgroup of F waves walks R consecutive
+// rows in lockstep, wave c owning column c: the far source of (r, c) is
+// (r - 1, c), the wave's own previous step, kept in registers; the near
+// sources t - 1, t - 2 are the neighbouring waves' rows of the same step (or
+// the previous step across the row boundary), passed through LDS.  Keys are
+// finalised two rows behind their query row, from the own queries (r - 2, c)
+// (self slot) and (r - 1, c) (far slot) in registers and the near queries'
+// q/dO rows and slot weights from LDS.  One barrier per step; every wave of
+// the workgroup runs the same number of steps.
+
+struct TcSlot {
+  u32x4 kv[4][2][64];     // [row & 3][k, v][lane]
+  u32x4 qd[4][2][64];     // [row & 3][q, dO][lane]
+  float4 w[4][16];        // [row & 3][head]: (p_1, scale dS_1, p_2, scale dS_2)
+};
+
+struct TcCfg {
+  int R;        // rows per workgroup
+  int blocks;   // row blocks per (batch, head group)
+  int HG, nwg;
+};
+
+template <typename T, int LPR, int NM, int F>
+struct BwdTc {
+  static constexpr int VEC = VecOf<T>::value;
+  static constexpr int NN = NearSet<NM>::count;
+  static constexpr int NS = NN + 1;
+  static constexpr int G = 64 / LPR;
+
+  Stream q, k, v, go, dq, dk, dv, lse;
+  float scale;
+  int T_, Tm1, r0, R, c, lane, hl, li;
+  TcSlot* lds;
+  Raw kr[4], vr[4], qr[4], gr[4];   // own rows by row & 3
+  float lr[4];
+  float p0[4], d0[4];               // own query's self-slot (p, scale dS) by row & 3
+  float pf[4], df[4];               // own query's far-slot (p, scale dS) by row & 3
+
+  template <int K>
+  __device__ inline void prefetch(int r) {
+    const int t = clampi(r * F + c, Tm1);
+    kr[K] = load_at(k, t);
+    vr[K] = load_at(v, t);
+    qr[K] = load_at(q, t);
+    gr[K] = load_at(go, t);
+    lr[K] = load_f32(lse, t);
+  }
+
+  __device__ static inline u32x4 pack(const Raw& x) { return u32x4{x.w[0], x.w[1], x.w[2], x.w[3]}; }
+  __device__ static inline Raw unpack(const u32x4& x) { return Raw{{x.x, x.y, x.z, x.w}}; }
+
+  // Step of row r (K = r & 3, static).
+  template <int K>
+  __device__ inline void step(int r) {
+    constexpr int K1 = (K + 3) & 3, K2 = (K + 2) & 3;   // rows r - 1, r - 2
+    TcSlot& me = lds[c];
+    me.kv[K][0][lane] = pack(kr[K]);
+    me.kv[K][1][lane] = pack(vr[K]);
+    me.qd[K][0][lane] = pack(qr[K]);
+    me.qd[K][1][lane] = pack(gr[K]);
+    __syncthreads();
+    const int t = r * F + c;
+    // ---- query (r, c): rows r0 .. r0 + R (row r0 + R feeds the last keys)
+    if (r >= r0 && r <= r0 + R) {
+      Raw kn[3], vn[3];
+      const Raw* ks[NS];
+      const Raw* vs[NS];
+      bool ok[NS];
+      int idx = 0;
+#pragma unroll
+      for (int n = 0; n < 3; ++n) {
+        if (NM & (1 << n)) {
+          if (n == 0) {
+            ks[idx] = &kr[K];
+            vs[idx] = &vr[K];
+          } else {
+            // Source t - n: wave c - n of this row, or wave c - n + F of row r - 1.
+            const bool wrap = c < n;
+            const int src = wrap ? c - n + F : c - n;
+            const TcSlot& o = lds[src];
+            kn[n] = unpack(wrap ? o.kv[K1][0][lane] : o.kv[K][0][lane]);
+            vn[n] = unpack(wrap ? o.kv[K1][1][lane] : o.kv[K][1][lane]);
+            ks[idx] = &kn[n];
+            vs[idx] = &vn[n];
+          }
+          ok[idx] = t - n >= 0;
+          ++idx;
+        }
+      }
+      ks[NS - 1] = &kr[K1];   // far source (r - 1, c)
+      vs[NS - 1] = &vr[K1];
+      ok[NS - 1] = t - F >= 0;
+      float pp[NS], ds[NS];
+      {
+        float dp[NS];
+        float delta = 0.f;
+#pragma unroll
+        for (int s_ = 0; s_ < NS; ++s_) {
+          const float sc = row_sum<LPR>(dot_raw<T>(qr[K], *ks[s_])) * scale;
+          dp[s_] = row_sum<LPR>(dot_raw<T>(gr[K], *vs[s_]));
+          pp[s_] = ok[s_] ? fast_exp(sc - lr[K]) : 0.f;
+          delta = __builtin_fmaf(pp[s_], dp[s_], delta);
+        }
+#pragma unroll
+        for (int s_ = 0; s_ < NS; ++s_) ds[s_] = pp[s_] * (dp[s_] - delta);
+      }
+      // Slot weights for the keys this query feeds: self (kept), far (kept),
+      // t - 1 and t - 2 (published for the owning waves).
+      p0[K] = pp[0];
+      d0[K] = ds[0] * scale;
+      pf[K] = pp[NS - 1];
+      df[K] = ds[NS - 1] * scale;
+      float4 wn = make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (NM & 2) {
+        wn.x = pp[1];
+        wn.y = ds[1] * scale;
+      }
+      if constexpr (NM & 4) {
+        constexpr int i2 = NearSet<NM>::count - 1;
+        wn.z = pp[i2];
+        wn.w = ds[i2] * scale;
+      }
+      if (li == 0) me.w[K][hl] = wn;
+      if (r < r0 + R && t < T_) {
+        float g[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) g[e] = 0.f;
+#pragma unroll
+        for (int s_ = 0; s_ < NS; ++s_) {
+          float kx[VEC];
+          widen<T>(*ks[s_], kx);
+          const float cc = ds[s_] * scale;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) g[e] = __builtin_fmaf(cc, kx[e], g[e]);
+        }
+        store_at<T>(dq, t, g);
+      }
+    }
+    // ---- key (r - 2, c)
+    const int rj = r - 2;
+    const int j = rj * F + c;
+    if (rj >= r0 && rj < r0 + R && j < T_) {
+      float ak[VEC], av[VEC];
+      float qx[VEC], gx[VEC];
+      // self slot: own query (r - 2, c)
+      {
+        const float cs = d0[K2];
+        const float cp = p0[K2];
+        widen<T>(qr[K2], qx);
+        widen<T>(gr[K2], gx);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          ak[e] = cs * qx[e];
+          av[e] = cp * gx[e];
+        }
+      }
+      // near slots n = 1, 2: query j + n = wave c + n of row r - 2, or wave
+      // c + n - F of row r - 1.
+#pragma unroll
+      for (int n = 1; n < 3; ++n) {
+        if (NM & (1 << n)) {
+          const bool wrap = c + n >= F;
+          const int src = wrap ? c + n - F : c + n;
+          const TcSlot& o = lds[src];
+          const float4 wq = wrap ? o.w[K1][hl] : o.w[K2][hl];
+          const bool there = j + n < T_;
+          const float cs = there ? (n == 1 ? wq.y : wq.w) : 0.f;
+          const float cp = there ? (n == 1 ? wq.x : wq.z) : 0.f;
+          const Raw qq = unpack(wrap ? o.qd[K1][0][lane] : o.qd[K2][0][lane]);
+          const Raw gg = unpack(wrap ? o.qd[K1][1][lane] : o.qd[K2][1][lane]);
+          widen<T>(qq, qx);
+          widen<T>(gg, gx);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            ak[e] = __builtin_fmaf(cs, qx[e], ak[e]);
+            av[e] = __builtin_fmaf(cp, gx[e], av[e]);
+          }
+        }
+      }
+      // far slot: own query (r - 1, c) = j + F
+      {
+        const bool there = j + F < T_;
+        const float cs = there ? df[K1] : 0.f;
+        const float cp = there ? pf[K1] : 0.f;
+        widen<T>(qr[K1], qx);
+        widen<T>(gr[K1], gx);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          ak[e] = __builtin_fmaf(cs, qx[e], ak[e]);
+          av[e] = __builtin_fmaf(cp, gx[e], av[e]);
+        }
+      }
+      store_at<T>(dk, j, ak);
+      store_at<T>(dv, j, av);
+    }
+  }
+};
+
+template <typename T, int LPR, int NM, int F>
+__global__ __launch_bounds__(64 * F) void bwd_tc(Params p, TcCfg cfg) {
+  __shared__ TcSlot lds[F];
+  const int c = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  int64_t g = xcd_remap(blockIdx.x, gridDim.x);
+  const int rb = (int)(g % cfg.blocks);
+  g /= cfg.blocks;
+  const int hg = (int)(g % cfg.HG);
+  const int b = (int)(g / cfg.HG);
+  constexpr int esz = (int)sizeof(T);
+  const int lane = threadIdx.x & 63;
+  const int hl = lane / LPR, li = lane % LPR;
+  const int h0 = hg * (64 / LPR);
+  BwdTc<T, LPR, NM, F> x;
+  x.q = make_stream(p.q, esz, b, h0, hl, li);
+  x.k = make_stream(p.k, esz, b, h0, hl, li);
+  x.v = make_stream(p.v, esz, b, h0, hl, li);
+  x.go = make_stream(p.dout, esz, b, h0, hl, li);
+  x.dq = make_stream(p.dq, esz, b, h0, hl, li);
+  x.dk = make_stream(p.dk, esz, b, h0, hl, li);
+  x.dv = make_stream(p.dv, esz, b, h0, hl, li);
+  x.lse = lse_stream(p, b, h0, hl);
+  x.scale = p.scale;
+  x.T_ = p.T;
+  x.Tm1 = p.T - 1;
+  x.R = cfg.R;
+  x.r0 = rb * cfg.R;
+  x.c = c;
+  x.lane = lane;
+  x.hl = hl;
+  x.li = li;
+  x.lds = lds;
+  // Rows r0-1 .. r0+R+1 (R + 3 steps, rounded up to a multiple of 4; the
+  // extra steps compute nothing).  Row & 3 is the static slot K.
+  const int s0 = x.r0 - 1;
+  const int steps = (cfg.R + 3 + 3) & ~3;
+  // s0 & 3 is not known statically: walk from the multiple of 4 below s0
+  // (steps before s0 compute nothing; they only fill the rotation).
+  const int sa = s0 & ~3;
+  const int sb = s0 + steps;
+  x.template prefetch<0>(sa);
+  for (int r = sa; r < sb; r += 4) {
+    x.template prefetch<1>(r + 1);
+    x.template step<0>(r);
+    x.template prefetch<2>(r + 2);
+    x.template step<1>(r + 1);
+    x.template prefetch<3>(r + 3);
+    x.template step<2>(r + 2);
+    x.template prefetch<0>(r + 4);
+    x.template step<3>(r + 3);
   }
 }
 
@@ -1475,18 +1745,47 @@ hipError_t launch_chain(const Params& p, const WalkCfg& wc, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <typename T, int LPR, int NM, int F>
+hipError_t launch_tc(const Params& p, const WalkCfg& wc, hipStream_t st) {
+  TcCfg c{};
+  const int64_t rows = (p.T + F - 1) / F;
+  const int64_t lanes_rows = (int64_t)p.B * wc.HG;
+  int R = 256;
+  while (R > 16 && lanes_rows * ((rows + R - 1) / R) < 1024) R >>= 1;
+  c.R = R;
+  c.blocks = (int)((rows + R - 1) / R);
+  c.HG = wc.HG;
+  const int64_t nwg = lanes_rows * c.blocks;
+  if (nwg <= 0 || nwg > 0x7fffffff) return hipErrorInvalidValue;
+  c.nwg = (int)nwg;
+  hipLaunchKernelGGL((bwd_tc<T, LPR, NM, F>), dim3((unsigned)c.nwg), dim3(64 * F), 0, st, p, c);
+  return hipGetLastError();
+}
+
 template <typename T, int LPR, bool PRO, bool FWD>
 hipError_t launch_pattern(const Params& p, const WalkCfg& c, const Pattern& pat, hipStream_t st) {
   const dim3 grid((unsigned)c.nwg), block(kWalkBlock);
   if (!FWD && !PRO && pat.far != 0 && c.column) {
     return pat.nm == 7 ? launch_chain<T, LPR, 7>(p, c, st) : launch_chain<T, LPR, 1>(p, c, st);
   }
+  if (!FWD && !PRO && (pat.far == 4 || pat.far == 8) && !c.column) {
+    if (pat.far == 4)
+      return pat.nm == 7 ? launch_tc<T, LPR, 7, 4>(p, c, st) : launch_tc<T, LPR, 1, 4>(p, c, st);
+    return pat.nm == 7 ? launch_tc<T, LPR, 7, 8>(p, c, st) : launch_tc<T, LPR, 1, 8>(p, c, st);
+  }
 #define SBDA_WALK_CASE(NMV, FARV)                                                            \
   if (pat.nm == NMV && (pat.far != 0) == FARV) {                                             \
     if (FWD && PRO) {                                                                        \
       hipLaunchKernelGGL((fwd_pipe_pro<T, LPR, NMV, FARV>), grid, block, 0, st, p, c);      \
     } else if (FWD) {                                                                        \
-      hipLaunchKernelGGL((fwd_pipe<T, LPR, NMV, FARV>), grid, block, kFwdLdsCap, st, p, c);     \
+      if (FARV && pat.far == 4 && !c.column)                                                 \
+        hipLaunchKernelGGL((fwd_pipe<T, LPR, NMV, FARV, FARV ? 4 : 0>), grid, block, kFwdLdsCap, \
+                           st, p, c);                                                        \
+      else if (FARV && pat.far == 8 && !c.column)                                            \
+        hipLaunchKernelGGL((fwd_pipe<T, LPR, NMV, FARV, FARV ? 8 : 0>), grid, block, kFwdLdsCap, \
+                           st, p, c);                                                        \
+      else                                                                                   \
+        hipLaunchKernelGGL((fwd_pipe<T, LPR, NMV, FARV, 0>), grid, block, kFwdLdsCap, st, p, c); \
     } else if (PRO) {                                                                        \
       hipLaunchKernelGGL((bwd_q_pro<T, LPR, NMV, FARV>), grid, block, 0, st, p, c);         \
       hipError_t e_ = hipGetLastError();                                                     \

@@ -294,8 +294,9 @@ def test_rope_table_matches_fp32_reference_angles():
 
 
 @pytest.mark.parametrize("t", [1, 2, 3, 5, 17, 300, 3000])
-@pytest.mark.parametrize("offs", [(0, 1), (0, 2), (0, 1, 2, 3), (0, 1, 2, 16), (0, 1, 2, 1024),
-                                  (0, 4), (2, 0, 1, 64)])
+@pytest.mark.parametrize("offs", [(0, 1), (0, 2), (0, 1, 2, 3), (0, 1, 2, 4), (0, 1, 2, 8),
+                                  (0, 1, 2, 16), (0, 1, 2, 1024), (0, 4), (0, 8),
+                                  (2, 0, 1, 64)])
 def test_tile_edges_and_offset_patterns(t, offs):
     # Lengths that are not multiples of the tile, the 3-step unroll or the far
     # offset; far offsets below, at and above the tile size (linear and
@@ -304,6 +305,23 @@ def test_tile_edges_and_offset_patterns(t, offs):
     _close(_fused(q, k, v, offs, g), _oracle(q, k, v, offs, g), LOW_TOL, f"T={t} {offs}")
     q, k, v, g = _inputs(1, t, 8, 64, torch.float32, seed=t * 37 + sum(offs))
     _close(_fused(q, k, v, offs, g), _oracle(q, k, v, offs, g), FP32_TOL, f"fp32 T={t} {offs}")
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, LOW_TOL), (torch.float16, LOW_TOL),
+                                       (torch.float32, FP32_TOL)])
+@pytest.mark.parametrize("b,h,d", [(2, 16, 64), (1, 32, 32), (1, 8, 128)])
+@pytest.mark.parametrize("offs", [(0, 1, 2, 4), (0, 1, 2, 8), (0, 1, 2, 16), (0, 1, 2, 256),
+                                  (0, 1, 2, 2048), (0, 8)])
+def test_walk_kernels_across_head_groups_and_row_widths(dtype, tol, b, h, d, offs):
+    # The walk kernels for every lanes-per-row width (16-byte chunks per row:
+    # 4, 8 or 16) and several head groups per position / batches, so each
+    # workgroup decode path (independent waves, lockstep column chains,
+    # transposed chains for far offsets 4 and 8) runs with more than one head
+    # group; T = 4100 is not a multiple of any tile, row or chain length.
+    t = 4100
+    q, k, v, g = _inputs(b, t, h, d, dtype, seed=h * 7 + d + sum(offs))
+    _close(_fused(q, k, v, offs, g), _oracle(q, k, v, offs, g), tol,
+           f"{dtype} B={b} H={h} D={d} {offs}")
 
 
 # ------------------------------------------------------------ module level

@@ -42,26 +42,37 @@ namespace sbda {
 
 namespace {
 
-constexpr int kWaves = 4;               // independent waves per workgroup
+constexpr int kWaves = 4;               // prologue walks: independent waves per workgroup
 constexpr int kWalkBlock = kWaves * 64;
 
-// Tiles per launch the tile size aims for (at least).
+// Tiles per launch the prologue walks' tile size aims for (at least).
 constexpr int kWalkTiles = 8192;
 
-// The forward walks are launched with this much (unused) LDS per workgroup so
-// that at most two 4-wave workgroups share a CU (2 waves per SIMD).  Measured
-// at T = 2^20: the forward runs ~4% faster than at the 4-7 waves per SIMD its
-// registers allow (fewer concurrent row streams per HBM channel); 1 or 3-4
-// waves per SIMD are slower.  The backward walks are register-limited to 2-4
-// waves per SIMD already and gain nothing from a cap.
-constexpr unsigned kFwdLdsCap = 65536;
+// Pipelined walks (fwd_pipe, bwd_pipe): 8-wave workgroups walking consecutive
+// tiles in lockstep (one barrier per unrolled iteration), launched with
+// 112 KiB of (otherwise unused) LDS so one workgroup runs per CU.  Linear
+// tiles are 32 positions, so a workgroup covers 256 consecutive positions
+// and the rows in flight across the chip stay within a compact window (~64
+// MiB per tensor at T = 2^20 instead of ~512 MiB).  Measured at T = 2^20,
+// D = 64, bf16: far-free backward 1.55 -> 1.42 ms, forward 0.86 -> 0.79 ms,
+// against 4-wave independent workgroups with 128-position tiles; without
+// the barrier or without the LDS cap most of the gain is lost.
+constexpr int kPipeWaves = 8;
+// Row stride (bytes between positions t and t + F) from which lockstep groups
+// hold at most 4 rows of a column.
+constexpr int64_t kBigStride = (int64_t)32 << 20;
+constexpr int kPipeBlock = kPipeWaves * 64;
+constexpr unsigned kPipeLds = 114688;
 
 struct WalkCfg {
+  int waves;     // waves per workgroup
   int P;         // positions per tile
   int HG;        // head groups (waves per position)
   int tiles_t;   // tiles per (batch, head group) along T
   int column;    // 1: column order (far offset F is a multiple of P)
   int rows;      // column order: ceil(T / F)
+  int rg;        // column order: rows per lockstep group (0: consecutive tiles are rows)
+  int bands;     // column order: F / P
   int F;         // far offset (0 if none)
   int nwg;       // workgroups in the grid
   int64_t total; // tiles in the grid
@@ -85,7 +96,16 @@ __device__ inline bool decode_tile(const Params& p, const WalkCfg& c, int64_t n,
   const int64_t rest = n / c.HG;
   const int k = (int)(rest % c.tiles_t);
   b = (int)(rest / c.tiles_t);
-  if (c.column) {
+  if (c.column && c.rg) {
+    // Groups of `waves` tiles: rg rows x (waves / rg) bands.
+    const int bg_size = c.waves / c.rg;
+    const int rowgroups = (c.rows + c.rg - 1) / c.rg;
+    const int g = k / c.waves, w = k % c.waves;
+    const int r = (g % rowgroups) * c.rg + w % c.rg;
+    const int cb = (g / rowgroups) * bg_size + w / c.rg;
+    if (r >= c.rows || cb >= c.bands) return false;
+    a = r * c.F + cb * c.P;
+  } else if (c.column) {
     const int r = k % c.rows, cb = k / c.rows;
     a = r * c.F + cb * c.P;
   } else {
@@ -247,15 +267,21 @@ struct WaveTile {
   int hl, li;   // this lane's head within the group, 16-byte chunk within the row
 };
 
+// Every wave of a lockstep workgroup must run the same number of steps, so a
+// wave without a tile (past the last tile or past the end of the sequence)
+// walks from a = T: clamped loads, nothing stored.
 template <int LPR>
-__device__ inline bool wave_tile(const Params& p, const WalkCfg& c, WaveTile& w) {
+__device__ inline void wave_tile(const Params& p, const WalkCfg& c, WaveTile& w) {
   const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const int64_t n = xcd_remap(blockIdx.x, gridDim.x) * kWaves + wv;
-  if (!decode_tile(p, c, n, w.b, w.hg, w.a)) return false;
+  const int64_t n = xcd_remap(blockIdx.x, gridDim.x) * c.waves + wv;
+  if (!decode_tile(p, c, n, w.b, w.hg, w.a)) {
+    w.b = 0;
+    w.hg = 0;
+    w.a = p.T;
+  }
   const int lane = threadIdx.x & 63;
   w.hl = lane / LPR;
   w.li = lane % LPR;
-  return true;
 }
 
 // FR > 0: the far offset is the compile-time constant FR (4 or 8) and the far
@@ -364,9 +390,9 @@ struct FwdPipe {
 };
 
 template <typename T, int LPR, int NM, bool FAR, int FR>
-__global__ __launch_bounds__(kWalkBlock) void fwd_pipe(Params p, WalkCfg c) {
+__global__ __launch_bounds__(kPipeBlock) void fwd_pipe(Params p, WalkCfg c) {
   WaveTile wt;
-  if (!wave_tile<LPR>(p, c, wt)) return;
+  wave_tile<LPR>(p, c, wt);
   constexpr int G = 64 / LPR, esz = (int)sizeof(T);
   const int h0 = wt.hg * G;
   using W = FwdPipe<T, LPR, NM, FAR, FR>;
@@ -384,9 +410,13 @@ __global__ __launch_bounds__(kWalkBlock) void fwd_pipe(Params p, WalkCfg c) {
   // The walk starts early enough to fill the rotation (2 positions, or FR
   // for a rotation far source); those steps store nothing.  Slot of
   // position t is (t - t0) % RD.
+  // The trip count depends only on P (same for every wave of the workgroup).
   const int t0 = a - (FR > 2 ? FR : 2);
   w.template prefetch<0>(t0);
-  for (int t = t0; t < end; t += W::RD) w.template steps<0>(t, a, end);
+  for (int t = t0; t < a + c.P; t += W::RD) {
+    __syncthreads();
+    w.template steps<0>(t, a, end);
+  }
 }
 
 template <typename T, int LPR, int NM, bool FAR>
@@ -553,9 +583,9 @@ struct BwdPipe {
 };
 
 template <typename T, int LPR, int NM, bool FAR>
-__global__ __launch_bounds__(kWalkBlock) void bwd_pipe(Params p, WalkCfg c) {
+__global__ __launch_bounds__(kPipeBlock) void bwd_pipe(Params p, WalkCfg c) {
   WaveTile wt;
-  if (!wave_tile<LPR>(p, c, wt)) return;
+  wave_tile<LPR>(p, c, wt);
   constexpr int G = 64 / LPR, esz = (int)sizeof(T);
   const int h0 = wt.hg * G;
   BwdPipe<T, LPR, NM, FAR> w;
@@ -573,10 +603,12 @@ __global__ __launch_bounds__(kWalkBlock) void bwd_pipe(Params p, WalkCfg c) {
   w.Tm1 = p.T - 1;
   w.a = wt.a;
   w.end = min(wt.a + c.P, p.T);
-  // Walk u = a-2 .. end+1 (slot of u is (u - a + 2) & 3).
-  const int u0 = wt.a - 2, last = w.end + 1;
+  // Walk u = a-2 .. a+P+1 (slot of u is (u - a + 2) & 3); the trip count
+  // depends only on P, the same for every wave of the workgroup.
+  const int u0 = wt.a - 2, last = wt.a + c.P + 1;
   w.template prefetch<0>(u0);
   for (int u = u0; u <= last; u += 4) {
+    __syncthreads();
     w.template prefetch<1>(u + 1);
     w.template compute<0>(u);
     w.template prefetch<2>(u + 2);
@@ -1693,8 +1725,51 @@ int walk_lpr(const Params& p, int dtype) {
   return lpr;
 }
 
+// Tile order shared by both configurations: column order when the far offset
+// is a multiple of the tile, linear otherwise.
+void order_tiles(const Params& p, const Pattern& pat, int64_t lanes_rows, WalkCfg& c) {
+  c.F = pat.far;
+  if (pat.far >= c.P && pat.far % c.P == 0) {
+    c.column = 1;
+    c.rows = (p.T + pat.far - 1) / pat.far;
+    c.bands = pat.far / c.P;
+    if (c.rg) {
+      const int bg_size = c.waves / c.rg;
+      c.tiles_t = ((c.rows + c.rg - 1) / c.rg) * c.rg *
+                  ((c.bands + bg_size - 1) / bg_size) * bg_size;
+    } else {
+      c.tiles_t = c.rows * c.bands;
+    }
+  } else {
+    c.column = 0;
+    c.rows = 0;
+    c.tiles_t = (p.T + c.P - 1) / c.P;
+  }
+  c.total = lanes_rows * c.tiles_t;
+  c.nwg = (int)((c.total + c.waves - 1) / c.waves);
+}
+
+// Pipelined walks and the chained backward: 32-position tiles, or min(128, F)
+// for a power-of-two far offset F >= 16 (column order, far rows one column
+// row away); halved (not below 16) while the grid has fewer than 256 full
+// workgroups.
+WalkCfg make_pipe_cfg(const Params& p, int lpr, const Pattern& pat) {
+  WalkCfg c{};
+  c.waves = kPipeWaves;
+  c.HG = p.H / (64 / lpr);
+  const int64_t lanes_rows = (int64_t)p.B * c.HG;
+  const bool pow2far = pat.far >= 16 && (pat.far & (pat.far - 1)) == 0;
+  int P = pow2far ? min(128, pat.far) : 32;
+  while (P > 16 && lanes_rows * ((p.T + P - 1) / P) < 256 * kPipeWaves) P >>= 1;
+  c.P = P;
+  order_tiles(p, pat, lanes_rows, c);
+  return c;
+}
+
+// Prologue walks: 4-wave independent workgroups, about kWalkTiles tiles.
 WalkCfg make_cfg(const Params& p, int lpr, const Pattern& pat) {
   WalkCfg c{};
+  c.waves = kWaves;
   c.HG = p.H / (64 / lpr);
   const int64_t lanes_rows = (int64_t)p.B * c.HG;
   // About 8192 tiles fill 256 CUs several times over; the tile is at least
@@ -1707,18 +1782,7 @@ WalkCfg make_cfg(const Params& p, int lpr, const Pattern& pat) {
   // backward's chained workgroups share through LDS.
   if (pat.far >= 16 && pat.far < P && (pat.far & (pat.far - 1)) == 0) P = pat.far;
   c.P = P;
-  c.F = pat.far;
-  if (pat.far >= P && pat.far % P == 0) {
-    c.column = 1;
-    c.rows = (p.T + pat.far - 1) / pat.far;
-    c.tiles_t = c.rows * (pat.far / P);
-  } else {
-    c.column = 0;
-    c.rows = 0;
-    c.tiles_t = (p.T + P - 1) / P;
-  }
-  c.total = lanes_rows * c.tiles_t;
-  c.nwg = (int)((c.total + kWaves - 1) / kWaves);
+  order_tiles(p, pat, lanes_rows, c);
   return c;
 }
 
@@ -1729,6 +1793,8 @@ hipError_t launch_chain(const Params& p, const WalkCfg& wc, hipStream_t st) {
   c.F = wc.F;
   c.rows = wc.rows;
   c.W = c.rows >= 8 ? 8 : c.rows >= 4 ? 4 : c.rows >= 2 ? 2 : 1;
+  // Same DRAM-channel limit as the forward's row groups (walk_launch).
+  if ((int64_t)wc.F * p.q.st * (int64_t)sizeof(T) >= kBigStride && c.W > 4) c.W = 4;
   c.bands = wc.F / wc.P;
   c.blocks = (c.rows + c.W - 1) / c.W;
   c.HG = wc.HG;
@@ -1764,7 +1830,6 @@ hipError_t launch_tc(const Params& p, const WalkCfg& wc, hipStream_t st) {
 
 template <typename T, int LPR, bool PRO, bool FWD>
 hipError_t launch_pattern(const Params& p, const WalkCfg& c, const Pattern& pat, hipStream_t st) {
-  const dim3 grid((unsigned)c.nwg), block(kWalkBlock);
   if (!FWD && !PRO && pat.far != 0 && c.column) {
     return pat.nm == 7 ? launch_chain<T, LPR, 7>(p, c, st) : launch_chain<T, LPR, 1>(p, c, st);
   }
@@ -1773,26 +1838,29 @@ hipError_t launch_pattern(const Params& p, const WalkCfg& c, const Pattern& pat,
       return pat.nm == 7 ? launch_tc<T, LPR, 7, 4>(p, c, st) : launch_tc<T, LPR, 1, 4>(p, c, st);
     return pat.nm == 7 ? launch_tc<T, LPR, 7, 8>(p, c, st) : launch_tc<T, LPR, 1, 8>(p, c, st);
   }
+  const dim3 grid((unsigned)c.nwg);
+  const dim3 wblock(kWalkBlock), pblock(kPipeBlock);
 #define SBDA_WALK_CASE(NMV, FARV)                                                            \
   if (pat.nm == NMV && (pat.far != 0) == FARV) {                                             \
     if (FWD && PRO) {                                                                        \
-      hipLaunchKernelGGL((fwd_pipe_pro<T, LPR, NMV, FARV>), grid, block, 0, st, p, c);      \
+      hipLaunchKernelGGL((fwd_pipe_pro<T, LPR, NMV, FARV>), grid, wblock, 0, st, p, c);     \
     } else if (FWD) {                                                                        \
       if (FARV && pat.far == 4 && !c.column)                                                 \
-        hipLaunchKernelGGL((fwd_pipe<T, LPR, NMV, FARV, FARV ? 4 : 0>), grid, block, kFwdLdsCap, \
-                           st, p, c);                                                        \
+        hipLaunchKernelGGL((fwd_pipe<T, LPR, NMV, FARV, FARV ? 4 : 0>), grid, pblock,       \
+                           kPipeLds, st, p, c);                                              \
       else if (FARV && pat.far == 8 && !c.column)                                            \
-        hipLaunchKernelGGL((fwd_pipe<T, LPR, NMV, FARV, FARV ? 8 : 0>), grid, block, kFwdLdsCap, \
-                           st, p, c);                                                        \
+        hipLaunchKernelGGL((fwd_pipe<T, LPR, NMV, FARV, FARV ? 8 : 0>), grid, pblock,       \
+                           kPipeLds, st, p, c);                                              \
       else                                                                                   \
-        hipLaunchKernelGGL((fwd_pipe<T, LPR, NMV, FARV, 0>), grid, block, kFwdLdsCap, st, p, c); \
+        hipLaunchKernelGGL((fwd_pipe<T, LPR, NMV, FARV, 0>), grid, dim3(64 * c.waves),       \
+                           kPipeLds / (kPipeWaves / c.waves), st, p, c);                     \
     } else if (PRO) {                                                                        \
-      hipLaunchKernelGGL((bwd_q_pro<T, LPR, NMV, FARV>), grid, block, 0, st, p, c);         \
+      hipLaunchKernelGGL((bwd_q_pro<T, LPR, NMV, FARV>), grid, wblock, 0, st, p, c);        \
       hipError_t e_ = hipGetLastError();                                                     \
       if (e_ != hipSuccess) return e_;                                                       \
-      hipLaunchKernelGGL((bwd_k_pro<T, LPR, NMV, FARV>), grid, block, 0, st, p, c);         \
+      hipLaunchKernelGGL((bwd_k_pro<T, LPR, NMV, FARV>), grid, wblock, 0, st, p, c);        \
     } else {                                                                                 \
-      hipLaunchKernelGGL((bwd_pipe<T, LPR, NMV, FARV>), grid, block, 0, st, p, c);          \
+      hipLaunchKernelGGL((bwd_pipe<T, LPR, NMV, FARV>), grid, pblock, kPipeLds, st, p, c);  \
     }                                                                                        \
     return hipGetLastError();                                                                \
   }
@@ -1802,6 +1870,10 @@ hipError_t launch_pattern(const Params& p, const WalkCfg& c, const Pattern& pat,
   SBDA_WALK_CASE(1, true)
 #undef SBDA_WALK_CASE
   return hipErrorInvalidValue;
+}
+
+int64_t far_stride_bytes(const Params& p, const Pattern& pat, int dtype) {
+  return (int64_t)pat.far * p.q.st * (dtype == kFP32 ? 4 : 2);
 }
 
 template <typename T>
@@ -1814,7 +1886,17 @@ hipError_t walk_launch(const Params& p, int dtype, bool pro, hipStream_t st) {
   Pattern pat;
   if (!classify(p, &pat)) return hipErrorInvalidValue;
   const int lpr = walk_lpr(p, dtype);
-  const WalkCfg c = make_cfg(p, lpr, pat);
+  // The prologue walks keep 4-wave independent workgroups; the others use
+  // the lockstep configuration.
+  WalkCfg c = pro ? make_cfg(p, lpr, pat) : make_pipe_cfg(p, lpr, pat);
+  // Lockstep waves on rows F positions apart: at a row stride of 32 MiB and
+  // more, eight of them at once collide in the DRAM channel mapping (the
+  // forward at T = 2^20 lost up to 30% at F = 2^16, 2^17), so a workgroup
+  // takes 4 rows x 2 bands instead.
+  if (FWD && !pro && c.column && c.rows > 4 && far_stride_bytes(p, pat, dtype) >= kBigStride) {
+    c.rg = 4;
+    order_tiles(p, pat, (int64_t)p.B * c.HG, c);
+  }
   auto go = [&](auto tag, auto lprc) -> hipError_t {
     using T = typename decltype(tag)::type;
     constexpr int L = decltype(lprc)::value;

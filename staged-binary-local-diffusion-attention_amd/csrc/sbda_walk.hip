@@ -42,13 +42,7 @@ namespace sbda {
 
 namespace {
 
-constexpr int kWaves = 4;               // prologue walks: independent waves per workgroup
-constexpr int kWalkBlock = kWaves * 64;
-
-// Tiles per launch the prologue walks' tile size aims for (at least).
-constexpr int kWalkTiles = 8192;
-
-// Pipelined walks (fwd_pipe, bwd_pipe): 8-wave workgroups walking consecutive
+// Pipelined walks (all but the chained backwards): 8-wave workgroups walking consecutive
 // tiles in lockstep (one barrier per unrolled iteration), launched with
 // 112 KiB of (otherwise unused) LDS so one workgroup runs per CU.  Linear
 // tiles are 32 positions, so a workgroup covers 256 consecutive positions
@@ -83,10 +77,6 @@ struct WalkCfg {
 __device__ inline int64_t xcd_remap(int wg, int nwg) {
   const int xcd = wg & 7, idx = wg >> 3, per = nwg >> 3, rem = nwg & 7;
   return (int64_t)xcd * per + min(xcd, rem) + idx;
-}
-
-__device__ inline int64_t wave_id() {
-  return xcd_remap(blockIdx.x, gridDim.x) * kWaves + (threadIdx.x >> 6);
 }
 
 __device__ inline bool decode_tile(const Params& p, const WalkCfg& c, int64_t n, int& b, int& hg,
@@ -1190,11 +1180,33 @@ __global__ __launch_bounds__(64 * F) void bwd_tc(Params p, TcCfg cfg) {
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-template <typename T, bool NT = false>
-__device__ inline Raw load_raw_split(const T* __restrict__ row, int li, int D) {
-  constexpr int HV = VecOf<T>::value / 2;
-  const u32x2* px = reinterpret_cast<const u32x2*>(row + li * HV);
-  const u32x2* py = reinterpret_cast<const u32x2*>(row + (D >> 1) + li * HV);
+// Split-layout rows: a lane holds HV elements of each half (byte offsets
+// lo and hi inside a position), so RoPE partners share a lane.
+struct SplitStream {
+  const char* base;
+  uint32_t st;
+  uint32_t lo, hi;
+
+  __device__ inline uint32_t at(int t) const { return (uint32_t)t * st; }
+};
+
+template <typename Vw>
+__device__ inline SplitStream make_split(const Vw& vw, int esz, int b, int h0, int hl, int li,
+                                         int D, int hv) {
+  SplitStream s;
+  s.base = (const char*)vw.p + ((int64_t)b * vw.sb + (int64_t)h0 * vw.sh) * esz;
+  s.st = (uint32_t)(vw.st * esz);
+  const uint32_t head = (uint32_t)((int64_t)hl * vw.sh * esz);
+  s.lo = head + (uint32_t)(li * hv * esz);
+  s.hi = head + (uint32_t)(((D >> 1) + li * hv) * esz);
+  return s;
+}
+
+template <bool NT = false>
+__device__ inline Raw load_split(const SplitStream& s, int t) {
+  const uint32_t r = s.at(t);
+  const u32x2* px = reinterpret_cast<const u32x2*>(s.base + (uint64_t)(r + s.lo));
+  const u32x2* py = reinterpret_cast<const u32x2*>(s.base + (uint64_t)(r + s.hi));
   u32x2 x, y;
   if constexpr (NT) {
     x = __builtin_nontemporal_load(px);
@@ -1206,17 +1218,16 @@ __device__ inline Raw load_raw_split(const T* __restrict__ row, int li, int D) {
   return Raw{{x.x, x.y, y.x, y.y}};
 }
 
-// Split-layout counterpart of store_raw (two 8-byte non-temporal stores).
 template <typename T>
-__device__ inline void store_split_nt(T* __restrict__ row, int li, int D,
-                                      const float (&x)[VecOf<T>::value]) {
+__device__ inline void store_split(const SplitStream& s, int t, const float (&x)[VecOf<T>::value]) {
   constexpr int HV = VecOf<T>::value / 2;
   uint32_t wa[2], wb[2];
   pack_words<T, 2>(x, wa);
   pack_words<T, 2>(x + HV, wb);
-  __builtin_nontemporal_store(u32x2{wa[0], wa[1]}, reinterpret_cast<u32x2*>(row + li * HV));
-  __builtin_nontemporal_store(u32x2{wb[0], wb[1]},
-                              reinterpret_cast<u32x2*>(row + (D >> 1) + li * HV));
+  const uint32_t r = s.at(t);
+  char* base = const_cast<char*>(s.base);
+  __builtin_nontemporal_store(u32x2{wa[0], wa[1]}, reinterpret_cast<u32x2*>(base + (uint64_t)(r + s.lo)));
+  __builtin_nontemporal_store(u32x2{wb[0], wb[1]}, reinterpret_cast<u32x2*>(base + (uint64_t)(r + s.hi)));
 }
 
 template <typename T, int LPR>
@@ -1224,8 +1235,7 @@ struct ProBase {
   static constexpr int VEC = VecOf<T>::value;
   static constexpr int HV = VEC / 2;
   using PL = Prologue<T, LPR>;
-  const float* __restrict__ rc;
-  const float* __restrict__ rs;
+  Stream rc, rs;   // fp32 [T, D/2] RoPE tables: this lane's HV entries of a position
   float eps;
   int li, D, Tm1;
   float wq[VEC], wk[VEC];
@@ -1234,14 +1244,30 @@ struct ProBase {
     li = lane_in_row;
     D = p.D;
     Tm1 = p.T - 1;
-    rc = p.rope_cos;
-    rs = p.rope_sin;
     eps = p.eps;
+    const int half = D >> 1;
+    rc.base = (const char*)p.rope_cos;
+    rs.base = (const char*)p.rope_sin;
+    rc.st = rs.st = (uint32_t)half * 4u;
+    rc.lane = rs.lane = (uint32_t)(li * HV) * 4u;
     PL::load_w(p.wq, li, D, wq);
     PL::load_w(p.wk, li, D, wk);
   }
+  // cos/sin of position t (every lane of a walk row is inside the row).
   __device__ inline void cs(int t, float (&c)[HV], float (&s)[HV]) const {
-    PL::load_cs(rc, rs, t, li, D, c, s);
+    const uint32_t oc = rc.at(t), os = rs.at(t);
+    if constexpr (HV == 4) {
+      const float4 a = *reinterpret_cast<const float4*>(rc.base + (uint64_t)oc);
+      const float4 b = *reinterpret_cast<const float4*>(rs.base + (uint64_t)os);
+      c[0] = a.x; c[1] = a.y; c[2] = a.z; c[3] = a.w;
+      s[0] = b.x; s[1] = b.y; s[2] = b.z; s[3] = b.w;
+    } else {
+      static_assert(HV == 2, "16-bit rows hold 4, fp32 rows 2 elements per half");
+      const float2 a = *reinterpret_cast<const float2*>(rc.base + (uint64_t)oc);
+      const float2 b = *reinterpret_cast<const float2*>(rs.base + (uint64_t)os);
+      c[0] = a.x; c[1] = a.y;
+      s[0] = b.x; s[1] = b.y;
+    }
   }
   // Widens a raw q/k row and applies the prologue; returns the rms factor.
   __device__ inline float rope(const Raw& r, const float (&w)[VEC], const float (&c)[HV],
@@ -1259,13 +1285,9 @@ struct FwdPipePro : ProBase<T, LPR> {
   static constexpr int NN = NearSet<NM>::count;
   static constexpr int NS = NN + (FAR ? 1 : 0);
 
-  const T* __restrict__ q;
-  const T* __restrict__ k;
-  const T* __restrict__ v;
-  T* __restrict__ o;
-  float* __restrict__ lse;
-  int64_t qst, kst, vst, ost;
-  int lst, F;
+  SplitStream q, k, v, o;
+  Stream lse;
+  int F;
   float scale;
   Raw kraw[2], qraw[2], vraw[2], klr[2], vlr[2];
   float cc[2][HV], ss[2][HV], clc[2][HV], cls[2][HV];
@@ -1274,14 +1296,14 @@ struct FwdPipePro : ProBase<T, LPR> {
   template <int R>
   __device__ inline void prefetch(int t) {
     const int tc = clampi(t, this->Tm1);
-    kraw[R & 1] = load_raw_split<T, !FAR>(k + (int64_t)tc * kst, this->li, this->D);
-    qraw[R & 1] = load_raw_split<T, !FAR>(q + (int64_t)tc * qst, this->li, this->D);
-    vraw[R & 1] = load_raw_split<T, !FAR>(v + (int64_t)tc * vst, this->li, this->D);
+    kraw[R & 1] = load_split<!FAR>(k, tc);
+    qraw[R & 1] = load_split<!FAR>(q, tc);
+    vraw[R & 1] = load_split<!FAR>(v, tc);
     this->cs(tc, cc[R & 1], ss[R & 1]);
     if constexpr (FAR) {
       const int tf = clampi(t - F, this->Tm1);
-      klr[R & 1] = load_raw_split<T>(k + (int64_t)tf * kst, this->li, this->D);
-      vlr[R & 1] = load_raw_split<T>(v + (int64_t)tf * vst, this->li, this->D);
+      klr[R & 1] = load_split(k, tf);
+      vlr[R & 1] = load_split(v, tf);
       this->cs(tf, clc[R & 1], cls[R & 1]);
     }
   }
@@ -1341,36 +1363,33 @@ struct FwdPipePro : ProBase<T, LPR> {
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[e] *= inv;
     if (store) {
-      store_split_nt<T>(o + (int64_t)t * ost, this->li, this->D, acc);
-      if (this->li == 0) lse[(int64_t)t * lst] = l > 0.f ? m + fast_log(l) : INFINITY;
+      store_split<T>(o, t, acc);
+      if (this->li == 0) store_f32(lse, t, l > 0.f ? m + fast_log(l) : INFINITY);
     }
   }
 };
 
 template <typename T, int LPR, int NM, bool FAR>
-__global__ __launch_bounds__(kWalkBlock) void fwd_pipe_pro(Params p, WalkCfg c) {
-  int b, hg, a;
-  if (!decode_tile(p, c, wave_id(), b, hg, a)) return;
-  const int lane = threadIdx.x & 63;
-  const int h = hg * (64 / LPR) + lane / LPR;
+__global__ __launch_bounds__(kPipeBlock) void fwd_pipe_pro(Params p, WalkCfg c) {
+  WaveTile wt;
+  wave_tile<LPR>(p, c, wt);
+  constexpr int esz = (int)sizeof(T);
+  const int h0 = wt.hg * (64 / LPR);
   FwdPipePro<T, LPR, NM, FAR> w;
-  w.init(p, lane % LPR);
-  w.q = reinterpret_cast<const T*>(p.q.p) + (int64_t)b * p.q.sb + (int64_t)h * p.q.sh;
-  w.k = reinterpret_cast<const T*>(p.k.p) + (int64_t)b * p.k.sb + (int64_t)h * p.k.sh;
-  w.v = reinterpret_cast<const T*>(p.v.p) + (int64_t)b * p.v.sb + (int64_t)h * p.v.sh;
-  w.o = reinterpret_cast<T*>(p.o.p) + (int64_t)b * p.o.sb + (int64_t)h * p.o.sh;
-  w.qst = p.q.st;
-  w.kst = p.k.st;
-  w.vst = p.v.st;
-  w.ost = p.o.st;
-  w.lse = p.lse + (int64_t)b * p.T * p.H + h;
-  w.lst = p.H;
+  w.init(p, wt.li);
+  w.q = make_split(p.q, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.k = make_split(p.k, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.v = make_split(p.v, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.o = make_split(p.o, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.lse = lse_stream(p, wt.b, h0, wt.hl);
   w.scale = p.scale;
   w.F = c.F;
-  const int end = min(a + c.P, p.T);
-  const int t0 = a - 2;   // slot of t is (t - a + 2) & 3
+  const int a = wt.a, end = min(a + c.P, p.T);
+  // Slot of t is (t - a + 2) & 3; the trip count depends only on P.
+  const int t0 = a - 2;
   w.template prefetch<0>(t0);
-  for (int t = t0; t < end; t += 4) {
+  for (int t = t0; t < a + c.P; t += 4) {
+    __syncthreads();
     w.template prefetch<1>(t + 1);
     w.template compute<0>(t, t >= a && t < end);
     w.template prefetch<2>(t + 2);
@@ -1393,15 +1412,11 @@ struct BwdQPro : ProBase<T, LPR> {
   static constexpr int NN = NearSet<NM>::count;
   static constexpr int NS = NN + (FAR ? 1 : 0);
 
-  const T* __restrict__ q;
-  const T* __restrict__ k;
-  const T* __restrict__ v;
-  const T* __restrict__ go;
-  T* __restrict__ dq;
-  const float* __restrict__ lse;
+  SplitStream q, k, v, go, dq;
+  Stream lse;
   float* __restrict__ tab;   // (p, scale * dS) per (row, slot)
-  int64_t qst, kst, vst, gst, dqst, tst;
-  int lst, F, a, end;
+  int64_t tst;
+  int F, a, end;
   float scale;
   Raw kraw[2], qraw[2], graw[2], klr[2], vlr[2];
   float lv[2];
@@ -1413,16 +1428,16 @@ struct BwdQPro : ProBase<T, LPR> {
   template <int R>
   __device__ inline void prefetch(int u) {
     const int uc = clampi(u, this->Tm1);
-    kraw[R & 1] = load_raw_split<T, !FAR>(k + (int64_t)uc * kst, this->li, this->D);
-    vr[R] = load_raw_split<T, !FAR>(v + (int64_t)uc * vst, this->li, this->D);
-    qraw[R & 1] = load_raw_split<T, !FAR>(q + (int64_t)uc * qst, this->li, this->D);
-    graw[R & 1] = load_raw_split<T, !FAR>(go + (int64_t)uc * gst, this->li, this->D);
-    lv[R & 1] = lse[(int64_t)uc * lst];
+    kraw[R & 1] = load_split<!FAR>(k, uc);
+    vr[R] = load_split<!FAR>(v, uc);
+    qraw[R & 1] = load_split<!FAR>(q, uc);
+    graw[R & 1] = load_split<!FAR>(go, uc);
+    lv[R & 1] = load_f32(lse, uc);
     this->cs(uc, cc[R & 1], ss[R & 1]);
     if constexpr (FAR) {
       const int ul = clampi(u - F, this->Tm1);
-      klr[R & 1] = load_raw_split<T>(k + (int64_t)ul * kst, this->li, this->D);
-      vlr[R & 1] = load_raw_split<T>(v + (int64_t)ul * vst, this->li, this->D);
+      klr[R & 1] = load_split(k, ul);
+      vlr[R & 1] = load_split(v, ul);
       this->cs(ul, clc[R & 1], cls[R & 1]);
     }
   }
@@ -1477,7 +1492,7 @@ struct BwdQPro : ProBase<T, LPR> {
         for (int e = 0; e < VEC; ++e) g[e] = __builtin_fmaf(ds[s], ks[s][e], g[e]);
       }
       PL::backward_w(g, qx, rq, this->wq, cc[R & 1], ss[R & 1], this->D, dw);
-      store_split_nt<T>(dq + (int64_t)u * dqst, this->li, this->D, g);
+      store_split<T>(dq, u, g);
       float* trow = tab + (int64_t)u * tst;
 #pragma unroll
       for (int vix = 0; vix < 2 * NS; ++vix) {
@@ -1499,13 +1514,9 @@ struct BwdKPro : ProBase<T, LPR> {
   static constexpr int NN = NearSet<NM>::count;
   static constexpr int NS = NN + (FAR ? 1 : 0);
 
-  const T* __restrict__ q;
-  const T* __restrict__ k;
-  const T* __restrict__ go;
-  T* __restrict__ dk;
-  T* __restrict__ dv;
+  SplitStream q, k, go, dk, dv;
   const float* __restrict__ tab;
-  int64_t qst, kst, gst, dkst, dvst, tst;
+  int64_t tst;
   int F, a, end, T_;
   Raw qraw[2], kraw[2], qir[2], gir[2];
   Raw gr[4];
@@ -1517,12 +1528,12 @@ struct BwdKPro : ProBase<T, LPR> {
   template <int R>
   __device__ inline void prefetch(int u) {
     const int uc = clampi(u, this->Tm1);
-    qraw[R & 1] = load_raw_split<T, !FAR>(q + (int64_t)uc * qst, this->li, this->D);
-    gr[R] = load_raw_split<T, !FAR>(go + (int64_t)uc * gst, this->li, this->D);
+    qraw[R & 1] = load_split<!FAR>(q, uc);
+    gr[R] = load_split<!FAR>(go, uc);
     this->cs(uc, cc[R & 1], ss[R & 1]);
     const int j = u - 2;
     const int jc = clampi(j, this->Tm1);
-    kraw[R & 1] = load_raw_split<T, !FAR>(k + (int64_t)jc * kst, this->li, this->D);
+    kraw[R & 1] = load_split<!FAR>(k, jc);
     this->cs(jc, ckc[R & 1], cks[R & 1]);
     int idx = 0;
 #pragma unroll
@@ -1539,8 +1550,8 @@ struct BwdKPro : ProBase<T, LPR> {
       const float* trow = tab + (int64_t)ic * tst;
       tp[R & 1][NS - 1] = trow[2 * (NS - 1)];
       td[R & 1][NS - 1] = trow[2 * (NS - 1) + 1];
-      qir[R & 1] = load_raw_split<T>(q + (int64_t)ic * qst, this->li, this->D);
-      gir[R & 1] = load_raw_split<T>(go + (int64_t)ic * gst, this->li, this->D);
+      qir[R & 1] = load_split(q, ic);
+      gir[R & 1] = load_split(go, ic);
       this->cs(ic, cic[R & 1], cis[R & 1]);
     }
   }
@@ -1588,16 +1599,18 @@ struct BwdKPro : ProBase<T, LPR> {
       widen<T>(kraw[R & 1], kx);
       const float rk = PL::rms_factor(kx, this->D, this->eps);
       PL::backward_w(ak, kx, rk, this->wk, ckc[R & 1], cks[R & 1], this->D, dw);
-      store_split_nt<T>(dk + (int64_t)j * dkst, this->li, this->D, ak);
-      store_split_nt<T>(dv + (int64_t)j * dvst, this->li, this->D, av);
+      store_split<T>(dk, j, ak);
+      store_split<T>(dv, j, av);
     }
   }
 };
 
+// Four steps per trip with one barrier (the workgroup walks in lockstep).
 template <typename W>
 __device__ inline void walk4(W& w, int first, int last) {
   w.template prefetch<0>(first);
   for (int u = first; u <= last; u += 4) {
+    __syncthreads();
     w.template prefetch<1>(u + 1);
     w.template compute<0>(u);
     w.template prefetch<2>(u + 2);
@@ -1609,82 +1622,63 @@ __device__ inline void walk4(W& w, int first, int last) {
   }
 }
 
-template <typename T, int LPR, int NM, bool FAR>
-__global__ __launch_bounds__(kWalkBlock) void bwd_q_pro(Params p, WalkCfg c) {
-  constexpr int VEC = VecOf<T>::value;
-  const int64_t wave = wave_id();
-  int b, hg, a;
-  const bool live = decode_tile(p, c, wave, b, hg, a);
-  const int lane = threadIdx.x & 63;
-  BwdQPro<T, LPR, NM, FAR> w;
-#pragma unroll
-  for (int e = 0; e < VEC; ++e) w.dw[e] = 0.f;
-  if (live) {
-    const int h = hg * (64 / LPR) + lane / LPR;
-    w.init(p, lane % LPR);
-    auto base = [&](const View& vw) {
-      return reinterpret_cast<const T*>(vw.p) + (int64_t)b * vw.sb + (int64_t)h * vw.sh;
-    };
-    w.q = base(p.q);
-    w.k = base(p.k);
-    w.v = base(p.v);
-    w.go = base(p.dout);
-    w.dq = reinterpret_cast<T*>(p.dq.p) + (int64_t)b * p.dq.sb + (int64_t)h * p.dq.sh;
-    w.qst = p.q.st;
-    w.kst = p.k.st;
-    w.vst = p.v.st;
-    w.gst = p.dout.st;
-    w.dqst = p.dq.st;
-    w.lse = p.lse + (int64_t)b * p.T * p.H + h;
-    w.lst = p.H;
-    w.tab = p.tab + ((int64_t)b * p.T * p.H + h) * (2 * w.NS);
-    w.tst = (int64_t)p.H * 2 * w.NS;
-    w.scale = p.scale;
-    w.F = c.F;
-    w.a = a;
-    w.end = min(a + c.P, p.T);
-    // Queries a-2, a-1 only fill the near-source rotation (slot of u is (u - a + 2) & 3).
-    walk4(w, a - 2, w.end - 1);
-  }
-  write_wave_partial<T, LPR, true>(w.dw, p.dwq_part, wave, p.D);
+__device__ inline int64_t pipe_wave_id(const WalkCfg& c) {
+  return xcd_remap(blockIdx.x, gridDim.x) * c.waves +
+         __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
 }
 
 template <typename T, int LPR, int NM, bool FAR>
-__global__ __launch_bounds__(kWalkBlock) void bwd_k_pro(Params p, WalkCfg c) {
-  constexpr int VEC = VecOf<T>::value;
-  const int64_t wave = wave_id();
-  int b, hg, a;
-  const bool live = decode_tile(p, c, wave, b, hg, a);
-  const int lane = threadIdx.x & 63;
+__global__ __launch_bounds__(kPipeBlock) void bwd_q_pro(Params p, WalkCfg c) {
+  constexpr int VEC = VecOf<T>::value, esz = (int)sizeof(T);
+  WaveTile wt;
+  wave_tile<LPR>(p, c, wt);
+  const int h0 = wt.hg * (64 / LPR);
+  BwdQPro<T, LPR, NM, FAR> w;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) w.dw[e] = 0.f;
+  w.init(p, wt.li);
+  w.q = make_split(p.q, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.k = make_split(p.k, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.v = make_split(p.v, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.go = make_split(p.dout, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.dq = make_split(p.dq, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.lse = lse_stream(p, wt.b, h0, wt.hl);
+  w.tab = p.tab + ((int64_t)wt.b * p.T * p.H + h0 + wt.hl) * (2 * w.NS);
+  w.tst = (int64_t)p.H * 2 * w.NS;
+  w.scale = p.scale;
+  w.F = c.F;
+  w.a = wt.a;
+  w.end = min(wt.a + c.P, p.T);
+  // Queries a-2, a-1 only fill the near-source rotation (slot of u is
+  // (u - a + 2) & 3); the trip count depends only on P.
+  walk4(w, wt.a - 2, wt.a + c.P - 1);
+  write_wave_partial<T, LPR, true>(w.dw, p.dwq_part, pipe_wave_id(c), p.D);
+}
+
+template <typename T, int LPR, int NM, bool FAR>
+__global__ __launch_bounds__(kPipeBlock) void bwd_k_pro(Params p, WalkCfg c) {
+  constexpr int VEC = VecOf<T>::value, esz = (int)sizeof(T);
+  WaveTile wt;
+  wave_tile<LPR>(p, c, wt);
+  const int h0 = wt.hg * (64 / LPR);
   BwdKPro<T, LPR, NM, FAR> w;
 #pragma unroll
   for (int e = 0; e < VEC; ++e) w.dw[e] = 0.f;
-  if (live) {
-    const int h = hg * (64 / LPR) + lane / LPR;
-    w.init(p, lane % LPR);
-    auto base = [&](const View& vw) {
-      return reinterpret_cast<const T*>(vw.p) + (int64_t)b * vw.sb + (int64_t)h * vw.sh;
-    };
-    w.q = base(p.q);
-    w.k = base(p.k);
-    w.go = base(p.dout);
-    w.dk = reinterpret_cast<T*>(p.dk.p) + (int64_t)b * p.dk.sb + (int64_t)h * p.dk.sh;
-    w.dv = reinterpret_cast<T*>(p.dv.p) + (int64_t)b * p.dv.sb + (int64_t)h * p.dv.sh;
-    w.qst = p.q.st;
-    w.kst = p.k.st;
-    w.gst = p.dout.st;
-    w.dkst = p.dk.st;
-    w.dvst = p.dv.st;
-    w.tab = p.tab + ((int64_t)b * p.T * p.H + h) * (2 * w.NS);
-    w.tst = (int64_t)p.H * 2 * w.NS;
-    w.F = c.F;
-    w.a = a;
-    w.end = min(a + c.P, p.T);
-    w.T_ = p.T;
-    // Walk u = a .. end+1 (slot of u is (u - a) & 3); key u - 2 is finished at step u.
-    walk4(w, a, w.end + 1);
-  }
-  write_wave_partial<T, LPR, true>(w.dw, p.dwk_part, wave, p.D);
+  w.init(p, wt.li);
+  w.q = make_split(p.q, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.k = make_split(p.k, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.go = make_split(p.dout, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.dk = make_split(p.dk, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.dv = make_split(p.dv, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.tab = p.tab + ((int64_t)wt.b * p.T * p.H + h0 + wt.hl) * (2 * w.NS);
+  w.tst = (int64_t)p.H * 2 * w.NS;
+  w.F = c.F;
+  w.a = wt.a;
+  w.end = min(wt.a + c.P, p.T);
+  w.T_ = p.T;
+  // Walk u = a .. a+P+1 (slot of u is (u - a) & 3); key u - 2 is finished at step u.
+  walk4(w, wt.a, wt.a + c.P + 1);
+  write_wave_partial<T, LPR, true>(w.dw, p.dwk_part, pipe_wave_id(c), p.D);
 }
 
 // ================================================================= dispatch
@@ -1766,26 +1760,6 @@ WalkCfg make_pipe_cfg(const Params& p, int lpr, const Pattern& pat) {
   return c;
 }
 
-// Prologue walks: 4-wave independent workgroups, about kWalkTiles tiles.
-WalkCfg make_cfg(const Params& p, int lpr, const Pattern& pat) {
-  WalkCfg c{};
-  c.waves = kWaves;
-  c.HG = p.H / (64 / lpr);
-  const int64_t lanes_rows = (int64_t)p.B * c.HG;
-  // About 8192 tiles fill 256 CUs several times over; the tile is at least
-  // 16 positions (halo overhead <= 2/16) and at most 256.
-  int P = 256;
-  while (P > 16 && lanes_rows * ((p.T + P - 1) / P) < kWalkTiles) P >>= 1;
-  // A far offset inside the tile would make a wave re-read rows it loaded F
-  // steps earlier, long evicted from L2.  With the tile shrunk to F the far
-  // rows belong to the neighbouring tile of the same column, which the
-  // backward's chained workgroups share through LDS.
-  if (pat.far >= 16 && pat.far < P && (pat.far & (pat.far - 1)) == 0) P = pat.far;
-  c.P = P;
-  order_tiles(p, pat, lanes_rows, c);
-  return c;
-}
-
 template <typename T, int LPR, int NM>
 hipError_t launch_chain(const Params& p, const WalkCfg& wc, hipStream_t st) {
   ChainCfg c{};
@@ -1839,11 +1813,11 @@ hipError_t launch_pattern(const Params& p, const WalkCfg& c, const Pattern& pat,
     return pat.nm == 7 ? launch_tc<T, LPR, 7, 8>(p, c, st) : launch_tc<T, LPR, 1, 8>(p, c, st);
   }
   const dim3 grid((unsigned)c.nwg);
-  const dim3 wblock(kWalkBlock), pblock(kPipeBlock);
+  const dim3 pblock(kPipeBlock);
 #define SBDA_WALK_CASE(NMV, FARV)                                                            \
   if (pat.nm == NMV && (pat.far != 0) == FARV) {                                             \
     if (FWD && PRO) {                                                                        \
-      hipLaunchKernelGGL((fwd_pipe_pro<T, LPR, NMV, FARV>), grid, wblock, 0, st, p, c);     \
+      hipLaunchKernelGGL((fwd_pipe_pro<T, LPR, NMV, FARV>), grid, pblock, kPipeLds, st, p, c); \
     } else if (FWD) {                                                                        \
       if (FARV && pat.far == 4 && !c.column)                                                 \
         hipLaunchKernelGGL((fwd_pipe<T, LPR, NMV, FARV, FARV ? 4 : 0>), grid, pblock,       \
@@ -1855,10 +1829,10 @@ hipError_t launch_pattern(const Params& p, const WalkCfg& c, const Pattern& pat,
         hipLaunchKernelGGL((fwd_pipe<T, LPR, NMV, FARV, 0>), grid, dim3(64 * c.waves),       \
                            kPipeLds / (kPipeWaves / c.waves), st, p, c);                     \
     } else if (PRO) {                                                                        \
-      hipLaunchKernelGGL((bwd_q_pro<T, LPR, NMV, FARV>), grid, wblock, 0, st, p, c);        \
+      hipLaunchKernelGGL((bwd_q_pro<T, LPR, NMV, FARV>), grid, pblock, kPipeLds, st, p, c); \
       hipError_t e_ = hipGetLastError();                                                     \
       if (e_ != hipSuccess) return e_;                                                       \
-      hipLaunchKernelGGL((bwd_k_pro<T, LPR, NMV, FARV>), grid, wblock, 0, st, p, c);        \
+      hipLaunchKernelGGL((bwd_k_pro<T, LPR, NMV, FARV>), grid, pblock, kPipeLds, st, p, c); \
     } else {                                                                                 \
       hipLaunchKernelGGL((bwd_pipe<T, LPR, NMV, FARV>), grid, pblock, kPipeLds, st, p, c);  \
     }                                                                                        \
@@ -1876,6 +1850,21 @@ int64_t far_stride_bytes(const Params& p, const Pattern& pat, int dtype) {
   return (int64_t)pat.far * p.q.st * (dtype == kFP32 ? 4 : 2);
 }
 
+// The configuration a walk launch uses (also sizes the prologue backward's
+// norm-weight partials).  Lockstep waves on rows F positions apart: at a row
+// stride of 32 MiB and more, eight of them at once collide in the DRAM channel
+// mapping (the forward at T = 2^20 lost up to 30% at F = 2^16, 2^17), so a
+// workgroup then takes 4 rows x 2 bands.  The chained backward has its own
+// limit (launch_chain).
+WalkCfg launch_cfg(const Params& p, int dtype, const Pattern& pat, int lpr, bool fwd, bool pro) {
+  WalkCfg c = make_pipe_cfg(p, lpr, pat);
+  if ((fwd || pro) && c.column && c.rows > 4 && far_stride_bytes(p, pat, dtype) >= kBigStride) {
+    c.rg = 4;
+    order_tiles(p, pat, (int64_t)p.B * c.HG, c);
+  }
+  return c;
+}
+
 template <typename T>
 struct TypeTag {
   using type = T;
@@ -1886,17 +1875,7 @@ hipError_t walk_launch(const Params& p, int dtype, bool pro, hipStream_t st) {
   Pattern pat;
   if (!classify(p, &pat)) return hipErrorInvalidValue;
   const int lpr = walk_lpr(p, dtype);
-  // The prologue walks keep 4-wave independent workgroups; the others use
-  // the lockstep configuration.
-  WalkCfg c = pro ? make_cfg(p, lpr, pat) : make_pipe_cfg(p, lpr, pat);
-  // Lockstep waves on rows F positions apart: at a row stride of 32 MiB and
-  // more, eight of them at once collide in the DRAM channel mapping (the
-  // forward at T = 2^20 lost up to 30% at F = 2^16, 2^17), so a workgroup
-  // takes 4 rows x 2 bands instead.
-  if (FWD && !pro && c.column && c.rows > 4 && far_stride_bytes(p, pat, dtype) >= kBigStride) {
-    c.rg = 4;
-    order_tiles(p, pat, (int64_t)p.B * c.HG, c);
-  }
+  const WalkCfg c = launch_cfg(p, dtype, pat, lpr, FWD, pro);
   auto go = [&](auto tag, auto lprc) -> hipError_t {
     using T = typename decltype(tag)::type;
     constexpr int L = decltype(lprc)::value;
@@ -1957,8 +1936,8 @@ hipError_t walk_backward(const Params& p, int dtype, bool pro, hipStream_t st) {
 void walk_partials(const Params& p, int dtype, int64_t* pq, int64_t* pk, int64_t* tab_floats) {
   Pattern pat;
   classify(p, &pat);
-  const WalkCfg c = make_cfg(p, walk_lpr(p, dtype), pat);
-  *pq = (int64_t)c.nwg * kWaves;
+  const WalkCfg c = launch_cfg(p, dtype, pat, walk_lpr(p, dtype), false, true);
+  *pq = (int64_t)c.nwg * c.waves;
   *pk = *pq;
   *tab_floats = (int64_t)p.B * p.T * p.H * 2 * p.S;
 }

@@ -1743,17 +1743,17 @@ void order_tiles(const Params& p, const Pattern& pat, int64_t lanes_rows, WalkCf
   c.nwg = (int)((c.total + c.waves - 1) / c.waves);
 }
 
-// Pipelined walks and the chained backward: 32-position tiles, or min(128, F)
-// for a power-of-two far offset F >= 16 (column order, far rows one column
-// row away); halved (not below 16) while the grid has fewer than 256 full
-// workgroups.
-WalkCfg make_pipe_cfg(const Params& p, int lpr, const Pattern& pat) {
+// Pipelined walks and the chained backward: 32-position tiles, or
+// min(max_col_tile, F) for a power-of-two far offset F >= 16 (column order,
+// far rows one column row away); halved (not below 16) while the grid has
+// fewer than 256 full workgroups.
+WalkCfg make_pipe_cfg(const Params& p, int lpr, const Pattern& pat, int max_col_tile) {
   WalkCfg c{};
   c.waves = kPipeWaves;
   c.HG = p.H / (64 / lpr);
   const int64_t lanes_rows = (int64_t)p.B * c.HG;
   const bool pow2far = pat.far >= 16 && (pat.far & (pat.far - 1)) == 0;
-  int P = pow2far ? min(128, pat.far) : 32;
+  int P = pow2far ? min(max_col_tile, pat.far) : 32;
   while (P > 16 && lanes_rows * ((p.T + P - 1) / P) < 256 * kPipeWaves) P >>= 1;
   c.P = P;
   order_tiles(p, pat, lanes_rows, c);
@@ -1857,7 +1857,22 @@ int64_t far_stride_bytes(const Params& p, const Pattern& pat, int dtype) {
 // workgroup then takes 4 rows x 2 bands.  The chained backward has its own
 // limit (launch_chain).
 WalkCfg launch_cfg(const Params& p, int dtype, const Pattern& pat, int lpr, bool fwd, bool pro) {
-  WalkCfg c = make_pipe_cfg(p, lpr, pat);
+  if (fwd && !pro && pat.far >= 128) {
+    // The forward needs no row chain: 64-position tiles in groups of 2 rows
+    // x 4 bands keep each workgroup's rows within two 256 KiB windows.
+    // Measured at T = 2^20 over layers 8-20: 16.8 ms of forwards against
+    // 17.3 ms with 8 rows x 128 positions per workgroup.
+    // (Fewer than 4 bands: more rows per group, so no wave is left idle.)
+    WalkCfg c = make_pipe_cfg(p, lpr, pat, 64);
+    if (c.column && c.rows >= 2) {
+      int rg = 2;
+      while (rg < kPipeWaves && rg * c.bands < kPipeWaves) rg <<= 1;
+      c.rg = rg;
+      order_tiles(p, pat, (int64_t)p.B * c.HG, c);
+    }
+    return c;
+  }
+  WalkCfg c = make_pipe_cfg(p, lpr, pat, 128);
   if ((fwd || pro) && c.column && c.rows > 4 && far_stride_bytes(p, pat, dtype) >= kBigStride) {
     c.rg = 4;
     order_tiles(p, pat, (int64_t)p.B * c.HG, c);

@@ -637,7 +637,10 @@ struct ChainSlot {
 };
 
 struct ChainCfg {
-  int P, F, rows, W, bands, blocks;   // blocks: row blocks (ceil(rows / W)) per band
+  int P, F, rows, W, bands;
+  int L;        // rows per chain; a workgroup holds W / L chains on adjacent bands
+  int blocks;   // row blocks (ceil(rows / L)) per band
+  int bgroups;  // band groups (ceil(bands / (W / L)))
   int HG, nwg;
 };
 
@@ -870,8 +873,8 @@ __device__ inline void chain_wave(const Params& p, const ChainCfg& c, ChainSlot*
   x.end = min(a + c.P, p.T);   // < a for a row past the end: nothing is stored
   x.lane = threadIdx.x & 63;
   x.mine = lds + w;
-  x.up = lds + (w > 0 ? w - 1 : 0);
-  x.down = lds + (w + 1 < c.W ? w + 1 : w);
+  x.up = lds + (LEFT_LDS ? w - 1 : w);
+  x.down = lds + (RIGHT_LDS ? w + 1 : w);
   // The trip count depends only on P: u = a-2 .. a+P+1 in steps of 4.
   x.end_u = a + c.P + 1;
   x.walk(a - 2);
@@ -881,27 +884,30 @@ template <typename T, int LPR, int NM, int W>
 __global__ __launch_bounds__(64 * W) void bwd_chain(Params p, ChainCfg c) {
   __shared__ ChainSlot lds[W];
   const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  // Workgroup -> (batch, head group, band, row block), XCD-contiguous.
+  // Workgroup -> (batch, head group, band group, row block), XCD-contiguous;
+  // wave w -> row w % L of the block, band w / L of the group.
   int64_t g = xcd_remap(blockIdx.x, gridDim.x);
   const int rb = (int)(g % c.blocks);
   g /= c.blocks;
-  const int cb = (int)(g % c.bands);
-  g /= c.bands;
+  const int bgi = (int)(g % c.bgroups);
+  g /= c.bgroups;
   const int hg = (int)(g % c.HG);
   const int b = (int)(g / c.HG);
-  const int r = rb * W + w;
-  // Rows past the end (the last row block is padded to W rows) start at T:
-  // their loads are clamped and they store nothing.
+  const int lr = w % c.L;
+  const int r = rb * c.L + lr;
+  const int cb = bgi * (W / c.L) + w / c.L;
+  // Rows past the end (row blocks are padded to L rows, band groups to W / L
+  // bands) start at T: their loads are clamped and they store nothing.
   const int64_t a64 = (int64_t)r * c.F + (int64_t)cb * c.P;
-  const int a = a64 < p.T ? (int)a64 : p.T;
+  const int a = (r < c.rows && cb < c.bands && a64 < p.T) ? (int)a64 : p.T;
   const int lane = threadIdx.x & 63;
   const int hl = lane / LPR, li = lane % LPR;
   const int h0 = hg * (64 / LPR);
-  if (W == 1) {
+  if (c.L == 1) {
     chain_wave<T, LPR, NM, false, false>(p, c, lds, w, b, h0, a, hl, li);
-  } else if (w == 0) {
+  } else if (lr == 0) {
     chain_wave<T, LPR, NM, false, true>(p, c, lds, w, b, h0, a, hl, li);
-  } else if (w == W - 1) {
+  } else if (lr == c.L - 1) {
     chain_wave<T, LPR, NM, true, false>(p, c, lds, w, b, h0, a, hl, li);
   } else {
     chain_wave<T, LPR, NM, true, true>(p, c, lds, w, b, h0, a, hl, li);
@@ -1769,10 +1775,14 @@ hipError_t launch_chain(const Params& p, const WalkCfg& wc, hipStream_t st) {
   c.W = c.rows >= 8 ? 8 : c.rows >= 4 ? 4 : c.rows >= 2 ? 2 : 1;
   // Same DRAM-channel limit as the forward's row groups (walk_launch).
   if ((int64_t)wc.F * p.q.st * (int64_t)sizeof(T) >= kBigStride && c.W > 4) c.W = 4;
+  // One chain per workgroup (L = W): shorter chains on more bands measured
+  // slower (backward 30.7 -> 32.0 ms per step at L = 4).
+  c.L = c.W;
   c.bands = wc.F / wc.P;
-  c.blocks = (c.rows + c.W - 1) / c.W;
+  c.blocks = (c.rows + c.L - 1) / c.L;
+  c.bgroups = (c.bands + c.W / c.L - 1) / (c.W / c.L);
   c.HG = wc.HG;
-  const int64_t nwg = (int64_t)p.B * c.HG * c.bands * c.blocks;
+  const int64_t nwg = (int64_t)p.B * c.HG * c.bgroups * c.blocks;
   if (nwg <= 0 || nwg > 0x7fffffff) return hipErrorInvalidValue;
   c.nwg = (int)nwg;
   const dim3 grid((unsigned)c.nwg), block(64 * c.W);

@@ -1,0 +1,184 @@
+// Forward walks (fwd_pipe): scores against the near rows and the far row,
+// softmax, O and one log-normaliser per row.  Reference semantics:
+// BiAttn/left_v2.py:313-405.
+
+#include "sbda_walk.h"
+
+namespace sbda {
+namespace walk {
+
+namespace {
+
+// FR > 0: the far offset is the compile-time constant FR (4 or 8) and the far
+// row is taken from the rotation (depth FR + 2) instead of being loaded: a
+// row loaded FR steps earlier is long gone from L2 at the streaming rate.
+template <typename T, int LPR, int NM, bool FAR, int FR>
+struct FwdPipe {
+  static constexpr int VEC = VecOf<T>::value;
+  static constexpr int NN = NearSet<NM>::count;
+  static constexpr int NS = NN + (FAR ? 1 : 0);
+  static constexpr int RD = FR > 0 ? FR + 2 : 4;   // rotation depth (even)
+  static_assert(FR == 0 || FAR, "a rotation far source needs a far slot");
+
+  Stream q, k, v, o, lse;
+  float scale;
+  int F, Tm1, li;
+  Raw kr[RD];           // k at t (slot R), t-1, ...; slot R+1 is being fetched
+  Raw vraw[2], qn[2];   // this step's v and q (stage R & 1)
+  Raw kl[2], vl[2];     // far source t - F (FR == 0)
+  float vr[RD][VEC];    // widened v rotation
+
+  template <int R>
+  __device__ inline void prefetch(int t) {
+    const int tc = clampi(t, Tm1);
+    kr[R] = load_at<!FAR>(k, tc);
+    vraw[R & 1] = load_at<!FAR>(v, tc);
+    qn[R & 1] = load_at<!FAR>(q, tc);
+    if constexpr (FAR && FR == 0) {
+      const int tf = clampi(t - F, Tm1);
+      kl[R & 1] = load_at(k, tf);
+      vl[R & 1] = load_at(v, tf);
+    }
+  }
+
+  template <int R>
+  __device__ inline void compute(int t, bool store) {
+    widen<T>(vraw[R & 1], vr[R]);
+    float sc[NS];
+    bool ok[NS];
+    int idx = 0;
+#pragma unroll
+    for (int n = 0; n < 3; ++n) {
+      if (NM & (1 << n)) {
+        ok[idx] = t - n >= 0;
+        sc[idx] = row_sum<LPR>(dot_raw<T>(qn[R & 1], kr[(R + RD - n) % RD])) * scale;
+        ++idx;
+      }
+    }
+    float vf[VEC];
+    if constexpr (FAR) {
+      ok[NS - 1] = t - F >= 0;
+      if constexpr (FR > 0) {
+        constexpr int sf = (R + RD - FR) % RD;
+        sc[NS - 1] = row_sum<LPR>(dot_raw<T>(qn[R & 1], kr[sf])) * scale;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) vf[e] = vr[sf][e];
+      } else {
+        sc[NS - 1] = row_sum<LPR>(dot_raw<T>(qn[R & 1], kl[R & 1])) * scale;
+        widen<T>(vl[R & 1], vf);
+      }
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) m = ok[s] ? fmaxf(m, sc[s]) : m;
+    float w[NS], l = 0.f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      w[s] = ok[s] ? fast_exp(sc[s] - m) : 0.f;
+      l += w[s];
+    }
+    float acc[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+    idx = 0;
+#pragma unroll
+    for (int n = 0; n < 3; ++n) {
+      if (NM & (1 << n)) {
+        const int slot = (R + RD - n) % RD;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] = __builtin_fmaf(w[idx], vr[slot][e], acc[e]);
+        ++idx;
+      }
+    }
+    if constexpr (FAR) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[e] = __builtin_fmaf(w[NS - 1], vf[e], acc[e]);
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] *= inv;
+    if (store) {
+      store_at<T>(o, t, acc);
+      if (li == 0) store_f32(lse, t, l > 0.f ? m + fast_log(l) : INFINITY);
+    }
+  }
+
+  // Steps R .. RD-1 of one trip around the rotation (position of slot 0 is t).
+  template <int R>
+  __device__ inline void steps(int t, int a, int end) {
+    if constexpr (R < RD) {
+      prefetch<(R + 1) % RD>(t + R + 1);
+      compute<R>(t + R, t + R >= a && t + R < end);
+      steps<R + 1>(t, a, end);
+    }
+  }
+};
+
+template <typename T, int LPR, int NM, bool FAR, int FR>
+__global__ __launch_bounds__(kPipeBlock) void fwd_pipe(Params p, WalkCfg c) {
+  WaveTile wt;
+  wave_tile<LPR>(p, c, wt);
+  constexpr int G = 64 / LPR, esz = (int)sizeof(T);
+  const int h0 = wt.hg * G;
+  using W = FwdPipe<T, LPR, NM, FAR, FR>;
+  W w;
+  w.q = make_stream(p.q, esz, wt.b, h0, wt.hl, wt.li);
+  w.k = make_stream(p.k, esz, wt.b, h0, wt.hl, wt.li);
+  w.v = make_stream(p.v, esz, wt.b, h0, wt.hl, wt.li);
+  w.o = make_stream(p.o, esz, wt.b, h0, wt.hl, wt.li);
+  w.lse = lse_stream(p, wt.b, h0, wt.hl);
+  w.scale = p.scale;
+  w.F = c.F;
+  w.Tm1 = p.T - 1;
+  w.li = wt.li;
+  const int a = wt.a, end = min(a + c.P, p.T);
+  // The walk starts early enough to fill the rotation (2 positions, or FR
+  // for a rotation far source); those steps store nothing.  Slot of
+  // position t is (t - t0) % RD.
+  // The trip count depends only on P (same for every wave of the workgroup).
+  const int t0 = a - (FR > 2 ? FR : 2);
+  w.template prefetch<0>(t0);
+  for (int t = t0; t < a + c.P; t += W::RD) {
+    __syncthreads();
+    w.template steps<0>(t, a, end);
+  }
+}
+
+
+}  // namespace
+
+template <typename T, int LPR, int NM, bool FAR>
+hipError_t fwd_pattern(const Params& p, const WalkCfg& c, const Pattern& pat, hipStream_t st) {
+  const dim3 grid((unsigned)c.nwg), block(64 * c.waves);
+  if constexpr (FAR) {
+    if (pat.far == 4 && !c.column) {
+      hipLaunchKernelGGL((fwd_pipe<T, LPR, NM, true, 4>), grid, block, kPipeLds, st, p, c);
+      return hipGetLastError();
+    }
+    if (pat.far == 8 && !c.column) {
+      hipLaunchKernelGGL((fwd_pipe<T, LPR, NM, true, 8>), grid, block, kPipeLds, st, p, c);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((fwd_pipe<T, LPR, NM, FAR, 0>), grid, block, kPipeLds, st, p, c);
+  return hipGetLastError();
+}
+
+hipError_t launch_fwd(const Params& p, const WalkCfg& c, const Pattern& pat, int dtype, int lpr,
+                      hipStream_t st) {
+  return by_type_lpr(dtype, lpr, [&](auto tag, auto lprc) -> hipError_t {
+    using T = typename decltype(tag)::type;
+    constexpr int L = decltype(lprc)::value;
+    if (pat.far == 0) {
+      if (pat.nm == 3) return fwd_pattern<T, L, 3, false>(p, c, pat, st);
+      if (pat.nm == 5) return fwd_pattern<T, L, 5, false>(p, c, pat, st);
+    } else {
+      if (pat.nm == 7) return fwd_pattern<T, L, 7, true>(p, c, pat, st);
+      if (pat.nm == 1) return fwd_pattern<T, L, 1, true>(p, c, pat, st);
+    }
+    return hipErrorInvalidValue;
+  });
+}
+
+}  // namespace walk
+}  // namespace sbda

@@ -1,0 +1,573 @@
+// Walks with the fused head-RMSNorm + RoPE prologue (BiAttn/left_v2.py:237-239,
+// BiAttn/attention_common.py:25-50,64-76): forward and the two-pass backward.
+
+#include "sbda_walk.h"
+
+namespace sbda {
+namespace walk {
+
+namespace {
+
+// ============================================== pipelined walks, fused prologue
+//
+// The prologue (head-RMSNorm + RoPE of q and k) is applied to each raw row
+// once, when it arrives; roped rows are kept in fp32.  Rows are in the split
+// layout (a lane holds the same positions of both halves, so RoPE partners
+// share a lane); v and dO stay raw and their dot products use v_dot2.
+//
+// The backward runs as two walks so that each fits in registers:
+//   A (query side): per query u, p_s and dS_s, dQ (through the transposed
+//     prologue) and, per (row, slot), the pair (p_s, scale * dS_s) into a
+//     workspace table [B, T, H, 2 * NS] (fp32);
+//   B (key side): per key j, dK/dV from queries j + n (near slots) and j + F
+//     (far slot) using that table -- no weight recomputation -- then dK
+//     through the transposed prologue.
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Split-layout rows: a lane holds HV elements of each half (byte offsets
+// lo and hi inside a position), so RoPE partners share a lane.
+struct SplitStream {
+  const char* base;
+  uint32_t st;
+  uint32_t lo, hi;
+
+  __device__ inline uint32_t at(int t) const { return (uint32_t)t * st; }
+};
+
+template <typename Vw>
+__device__ inline SplitStream make_split(const Vw& vw, int esz, int b, int h0, int hl, int li,
+                                         int D, int hv) {
+  SplitStream s;
+  s.base = (const char*)vw.p + ((int64_t)b * vw.sb + (int64_t)h0 * vw.sh) * esz;
+  s.st = (uint32_t)(vw.st * esz);
+  const uint32_t head = (uint32_t)((int64_t)hl * vw.sh * esz);
+  s.lo = head + (uint32_t)(li * hv * esz);
+  s.hi = head + (uint32_t)(((D >> 1) + li * hv) * esz);
+  return s;
+}
+
+template <bool NT = false>
+__device__ inline Raw load_split(const SplitStream& s, int t) {
+  const uint32_t r = s.at(t);
+  const u32x2* px = reinterpret_cast<const u32x2*>(s.base + (uint64_t)(r + s.lo));
+  const u32x2* py = reinterpret_cast<const u32x2*>(s.base + (uint64_t)(r + s.hi));
+  u32x2 x, y;
+  if constexpr (NT) {
+    x = __builtin_nontemporal_load(px);
+    y = __builtin_nontemporal_load(py);
+  } else {
+    x = *px;
+    y = *py;
+  }
+  return Raw{{x.x, x.y, y.x, y.y}};
+}
+
+template <typename T>
+__device__ inline void store_split(const SplitStream& s, int t, const float (&x)[VecOf<T>::value]) {
+  constexpr int HV = VecOf<T>::value / 2;
+  uint32_t wa[2], wb[2];
+  pack_words<T, 2>(x, wa);
+  pack_words<T, 2>(x + HV, wb);
+  const uint32_t r = s.at(t);
+  char* base = const_cast<char*>(s.base);
+  __builtin_nontemporal_store(u32x2{wa[0], wa[1]}, reinterpret_cast<u32x2*>(base + (uint64_t)(r + s.lo)));
+  __builtin_nontemporal_store(u32x2{wb[0], wb[1]}, reinterpret_cast<u32x2*>(base + (uint64_t)(r + s.hi)));
+}
+
+template <typename T, int LPR>
+struct ProBase {
+  static constexpr int VEC = VecOf<T>::value;
+  static constexpr int HV = VEC / 2;
+  using PL = Prologue<T, LPR>;
+  Stream rc, rs;   // fp32 [T, D/2] RoPE tables: this lane's HV entries of a position
+  float eps;
+  int li, D, Tm1;
+  float wq[VEC], wk[VEC];
+
+  __device__ inline void init(const Params& p, int lane_in_row) {
+    li = lane_in_row;
+    D = p.D;
+    Tm1 = p.T - 1;
+    eps = p.eps;
+    const int half = D >> 1;
+    rc.base = (const char*)p.rope_cos;
+    rs.base = (const char*)p.rope_sin;
+    rc.st = rs.st = (uint32_t)half * 4u;
+    rc.lane = rs.lane = (uint32_t)(li * HV) * 4u;
+    PL::load_w(p.wq, li, D, wq);
+    PL::load_w(p.wk, li, D, wk);
+  }
+  // cos/sin of position t (every lane of a walk row is inside the row).
+  __device__ inline void cs(int t, float (&c)[HV], float (&s)[HV]) const {
+    const uint32_t oc = rc.at(t), os = rs.at(t);
+    if constexpr (HV == 4) {
+      const float4 a = *reinterpret_cast<const float4*>(rc.base + (uint64_t)oc);
+      const float4 b = *reinterpret_cast<const float4*>(rs.base + (uint64_t)os);
+      c[0] = a.x; c[1] = a.y; c[2] = a.z; c[3] = a.w;
+      s[0] = b.x; s[1] = b.y; s[2] = b.z; s[3] = b.w;
+    } else {
+      static_assert(HV == 2, "16-bit rows hold 4, fp32 rows 2 elements per half");
+      const float2 a = *reinterpret_cast<const float2*>(rc.base + (uint64_t)oc);
+      const float2 b = *reinterpret_cast<const float2*>(rs.base + (uint64_t)os);
+      c[0] = a.x; c[1] = a.y;
+      s[0] = b.x; s[1] = b.y;
+    }
+  }
+  // Widens a raw q/k row and applies the prologue; returns the rms factor.
+  __device__ inline float rope(const Raw& r, const float (&w)[VEC], const float (&c)[HV],
+                               const float (&s)[HV], float (&x)[VEC]) const {
+    widen<T>(r, x);
+    return PL::forward_w(x, w, c, s, D, eps);
+  }
+};
+
+template <typename T, int LPR, int NM, bool FAR>
+struct FwdPipePro : ProBase<T, LPR> {
+  using B_ = ProBase<T, LPR>;
+  using B_::VEC;
+  using B_::HV;
+  static constexpr int NN = NearSet<NM>::count;
+  static constexpr int NS = NN + (FAR ? 1 : 0);
+
+  SplitStream q, k, v, o;
+  Stream lse;
+  int F;
+  float scale;
+  Raw kraw[2], qraw[2], vraw[2], klr[2], vlr[2];
+  float cc[2][HV], ss[2][HV], clc[2][HV], cls[2][HV];
+  float kq[4][VEC], vr[4][VEC];
+
+  template <int R>
+  __device__ inline void prefetch(int t) {
+    const int tc = clampi(t, this->Tm1);
+    kraw[R & 1] = load_split<!FAR>(k, tc);
+    qraw[R & 1] = load_split<!FAR>(q, tc);
+    vraw[R & 1] = load_split<!FAR>(v, tc);
+    this->cs(tc, cc[R & 1], ss[R & 1]);
+    if constexpr (FAR) {
+      const int tf = clampi(t - F, this->Tm1);
+      klr[R & 1] = load_split(k, tf);
+      vlr[R & 1] = load_split(v, tf);
+      this->cs(tf, clc[R & 1], cls[R & 1]);
+    }
+  }
+
+  template <int R>
+  __device__ inline void compute(int t, bool store) {
+    this->rope(kraw[R & 1], this->wk, cc[R & 1], ss[R & 1], kq[R]);
+    widen<T>(vraw[R & 1], vr[R]);
+    float qr[VEC];
+    this->rope(qraw[R & 1], this->wq, cc[R & 1], ss[R & 1], qr);
+    float sc[NS];
+    bool ok[NS];
+    int idx = 0;
+#pragma unroll
+    for (int n = 0; n < 3; ++n) {
+      if (NM & (1 << n)) {
+        ok[idx] = t - n >= 0;
+        sc[idx] = row_sum<LPR>(dot_partial<VEC>(qr, kq[(R + 4 - n) & 3])) * scale;
+        ++idx;
+      }
+    }
+    float vf[VEC];
+    if constexpr (FAR) {
+      float kf[VEC];
+      this->rope(klr[R & 1], this->wk, clc[R & 1], cls[R & 1], kf);
+      widen<T>(vlr[R & 1], vf);
+      ok[NS - 1] = t - F >= 0;
+      sc[NS - 1] = row_sum<LPR>(dot_partial<VEC>(qr, kf)) * scale;
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) m = ok[s] ? fmaxf(m, sc[s]) : m;
+    float w[NS], l = 0.f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      w[s] = ok[s] ? fast_exp(sc[s] - m) : 0.f;
+      l += w[s];
+    }
+    float acc[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+    idx = 0;
+#pragma unroll
+    for (int n = 0; n < 3; ++n) {
+      if (NM & (1 << n)) {
+        const int slot = (R + 4 - n) & 3;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] = __builtin_fmaf(w[idx], vr[slot][e], acc[e]);
+        ++idx;
+      }
+    }
+    if constexpr (FAR) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[e] = __builtin_fmaf(w[NS - 1], vf[e], acc[e]);
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] *= inv;
+    if (store) {
+      store_split<T>(o, t, acc);
+      if (this->li == 0) store_f32(lse, t, l > 0.f ? m + fast_log(l) : INFINITY);
+    }
+  }
+};
+
+template <typename T, int LPR, int NM, bool FAR>
+__global__ __launch_bounds__(kPipeBlock) void fwd_pipe_pro(Params p, WalkCfg c) {
+  WaveTile wt;
+  wave_tile<LPR>(p, c, wt);
+  constexpr int esz = (int)sizeof(T);
+  const int h0 = wt.hg * (64 / LPR);
+  FwdPipePro<T, LPR, NM, FAR> w;
+  w.init(p, wt.li);
+  w.q = make_split(p.q, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.k = make_split(p.k, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.v = make_split(p.v, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.o = make_split(p.o, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.lse = lse_stream(p, wt.b, h0, wt.hl);
+  w.scale = p.scale;
+  w.F = c.F;
+  const int a = wt.a, end = min(a + c.P, p.T);
+  // Slot of t is (t - a + 2) & 3; the trip count depends only on P.
+  const int t0 = a - 2;
+  w.template prefetch<0>(t0);
+  for (int t = t0; t < a + c.P; t += 4) {
+    __syncthreads();
+    w.template prefetch<1>(t + 1);
+    w.template compute<0>(t, t >= a && t < end);
+    w.template prefetch<2>(t + 2);
+    w.template compute<1>(t + 1, t + 1 >= a && t + 1 < end);
+    w.template prefetch<3>(t + 3);
+    w.template compute<2>(t + 2, t + 2 >= a && t + 2 < end);
+    w.template prefetch<0>(t + 4);
+    w.template compute<3>(t + 3, t + 3 >= a && t + 3 < end);
+  }
+}
+
+// ---- backward A: query side
+
+template <typename T, int LPR, int NM, bool FAR>
+struct BwdQPro : ProBase<T, LPR> {
+  using B_ = ProBase<T, LPR>;
+  using B_::VEC;
+  using B_::HV;
+  using PL = typename B_::PL;
+  static constexpr int NN = NearSet<NM>::count;
+  static constexpr int NS = NN + (FAR ? 1 : 0);
+
+  SplitStream q, k, v, go, dq;
+  Stream lse;
+  float* __restrict__ tab;   // (p, scale * dS) per (row, slot)
+  int64_t tst;
+  int F, a, end;
+  float scale;
+  Raw kraw[2], qraw[2], graw[2], klr[2], vlr[2];
+  float lv[2];
+  float cc[2][HV], ss[2][HV], clc[2][HV], cls[2][HV];
+  float kq[4][VEC];
+  Raw vr[4];
+  float dw[VEC];
+
+  template <int R>
+  __device__ inline void prefetch(int u) {
+    const int uc = clampi(u, this->Tm1);
+    kraw[R & 1] = load_split<!FAR>(k, uc);
+    vr[R] = load_split<!FAR>(v, uc);
+    qraw[R & 1] = load_split<!FAR>(q, uc);
+    graw[R & 1] = load_split<!FAR>(go, uc);
+    lv[R & 1] = load_f32(lse, uc);
+    this->cs(uc, cc[R & 1], ss[R & 1]);
+    if constexpr (FAR) {
+      const int ul = clampi(u - F, this->Tm1);
+      klr[R & 1] = load_split(k, ul);
+      vlr[R & 1] = load_split(v, ul);
+      this->cs(ul, clc[R & 1], cls[R & 1]);
+    }
+  }
+
+  template <int R>
+  __device__ inline void compute(int u) {
+    this->rope(kraw[R & 1], this->wk, cc[R & 1], ss[R & 1], kq[R]);
+    float qx[VEC], qr[VEC];
+    widen<T>(qraw[R & 1], qx);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) qr[e] = qx[e];
+    const float rq = PL::forward_w(qr, this->wq, cc[R & 1], ss[R & 1], this->D, this->eps);
+    float kf[VEC];
+    if constexpr (FAR) this->rope(klr[R & 1], this->wk, clc[R & 1], cls[R & 1], kf);
+    const float* ks[NS];
+    const Raw* vs[NS];
+    bool ok[NS];
+    int idx = 0;
+#pragma unroll
+    for (int n = 0; n < 3; ++n) {
+      if (NM & (1 << n)) {
+        ks[idx] = kq[(R + 4 - n) & 3];
+        vs[idx] = &vr[(R + 4 - n) & 3];
+        ok[idx] = u - n >= 0;
+        ++idx;
+      }
+    }
+    if constexpr (FAR) {
+      ks[NS - 1] = kf;
+      vs[NS - 1] = &vlr[R & 1];
+      ok[NS - 1] = u - F >= 0;
+    }
+    float pp[NS], dp[NS], delta = 0.f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      float a_ = 0.f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) a_ = __builtin_fmaf(qr[e], ks[s][e], a_);
+      const float sc = row_sum<LPR>(a_) * scale;
+      dp[s] = row_sum<LPR>(dot_raw<T>(graw[R & 1], *vs[s]));
+      pp[s] = ok[s] ? fast_exp(sc - lv[R & 1]) : 0.f;
+      delta = __builtin_fmaf(pp[s], dp[s], delta);
+    }
+    if (u >= a && u < end) {
+      float g[VEC], ds[NS];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) g[e] = 0.f;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        ds[s] = pp[s] * (dp[s] - delta) * scale;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) g[e] = __builtin_fmaf(ds[s], ks[s][e], g[e]);
+      }
+      PL::backward_w(g, qx, rq, this->wq, cc[R & 1], ss[R & 1], this->D, dw);
+      store_split<T>(dq, u, g);
+      float* trow = tab + (int64_t)u * tst;
+#pragma unroll
+      for (int vix = 0; vix < 2 * NS; ++vix) {
+        const int s = vix >> 1;
+        if (vix % LPR == this->li) trow[vix] = (vix & 1) ? ds[s] : pp[s];
+      }
+    }
+  }
+};
+
+// ---- backward B: key side
+
+template <typename T, int LPR, int NM, bool FAR>
+struct BwdKPro : ProBase<T, LPR> {
+  using B_ = ProBase<T, LPR>;
+  using B_::VEC;
+  using B_::HV;
+  using PL = typename B_::PL;
+  static constexpr int NN = NearSet<NM>::count;
+  static constexpr int NS = NN + (FAR ? 1 : 0);
+
+  SplitStream q, k, go, dk, dv;
+  const float* __restrict__ tab;
+  int64_t tst;
+  int F, a, end, T_;
+  Raw qraw[2], kraw[2], qir[2], gir[2];
+  Raw gr[4];
+  float cc[2][HV], ss[2][HV], cic[2][HV], cis[2][HV], ckc[2][HV], cks[2][HV];
+  float tp[2][NS], td[2][NS];   // (p, scale dS) feeding key u - 2, per slot
+  float qq[4][VEC];
+  float dw[VEC];
+
+  template <int R>
+  __device__ inline void prefetch(int u) {
+    const int uc = clampi(u, this->Tm1);
+    qraw[R & 1] = load_split<!FAR>(q, uc);
+    gr[R] = load_split<!FAR>(go, uc);
+    this->cs(uc, cc[R & 1], ss[R & 1]);
+    const int j = u - 2;
+    const int jc = clampi(j, this->Tm1);
+    kraw[R & 1] = load_split<!FAR>(k, jc);
+    this->cs(jc, ckc[R & 1], cks[R & 1]);
+    int idx = 0;
+#pragma unroll
+    for (int n = 0; n < 3; ++n) {
+      if (NM & (1 << n)) {
+        const float* trow = tab + (int64_t)clampi(j + n, this->Tm1) * tst;
+        tp[R & 1][idx] = trow[2 * idx];
+        td[R & 1][idx] = trow[2 * idx + 1];
+        ++idx;
+      }
+    }
+    if constexpr (FAR) {
+      const int ic = clampi(j + F, this->Tm1);
+      const float* trow = tab + (int64_t)ic * tst;
+      tp[R & 1][NS - 1] = trow[2 * (NS - 1)];
+      td[R & 1][NS - 1] = trow[2 * (NS - 1) + 1];
+      qir[R & 1] = load_split(q, ic);
+      gir[R & 1] = load_split(go, ic);
+      this->cs(ic, cic[R & 1], cis[R & 1]);
+    }
+  }
+
+  template <int R>
+  __device__ inline void compute(int u) {
+    this->rope(qraw[R & 1], this->wq, cc[R & 1], ss[R & 1], qq[R]);
+    const int j = u - 2;
+    if (j >= a && j < end) {
+      float ak[VEC], av[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) { ak[e] = 0.f; av[e] = 0.f; }
+      int idx = 0;
+#pragma unroll
+      for (int n = 0; n < 3; ++n) {
+        if (NM & (1 << n)) {
+          const int slot = (R + 2 + n) & 3;   // query j + n
+          const bool there = j + n < T_;
+          const float cs_ = there ? td[R & 1][idx] : 0.f;
+          const float cp_ = there ? tp[R & 1][idx] : 0.f;
+          float gx[VEC];
+          widen<T>(gr[slot], gx);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            ak[e] = __builtin_fmaf(cs_, qq[slot][e], ak[e]);
+            av[e] = __builtin_fmaf(cp_, gx[e], av[e]);
+          }
+          ++idx;
+        }
+      }
+      if constexpr (FAR) {
+        const bool there = j + F < T_;
+        const float cs_ = there ? td[R & 1][NS - 1] : 0.f;
+        const float cp_ = there ? tp[R & 1][NS - 1] : 0.f;
+        float qf[VEC], gx[VEC];
+        this->rope(qir[R & 1], this->wq, cic[R & 1], cis[R & 1], qf);
+        widen<T>(gir[R & 1], gx);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          ak[e] = __builtin_fmaf(cs_, qf[e], ak[e]);
+          av[e] = __builtin_fmaf(cp_, gx[e], av[e]);
+        }
+      }
+      float kx[VEC];
+      widen<T>(kraw[R & 1], kx);
+      const float rk = PL::rms_factor(kx, this->D, this->eps);
+      PL::backward_w(ak, kx, rk, this->wk, ckc[R & 1], cks[R & 1], this->D, dw);
+      store_split<T>(dk, j, ak);
+      store_split<T>(dv, j, av);
+    }
+  }
+};
+
+// Four steps per trip with one barrier (the workgroup walks in lockstep).
+template <typename W>
+__device__ inline void walk4(W& w, int first, int last) {
+  w.template prefetch<0>(first);
+  for (int u = first; u <= last; u += 4) {
+    __syncthreads();
+    w.template prefetch<1>(u + 1);
+    w.template compute<0>(u);
+    w.template prefetch<2>(u + 2);
+    w.template compute<1>(u + 1);
+    w.template prefetch<3>(u + 3);
+    w.template compute<2>(u + 2);
+    w.template prefetch<0>(u + 4);
+    w.template compute<3>(u + 3);
+  }
+}
+
+__device__ inline int64_t pipe_wave_id(const WalkCfg& c) {
+  return xcd_remap(blockIdx.x, gridDim.x) * c.waves +
+         __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
+
+template <typename T, int LPR, int NM, bool FAR>
+__global__ __launch_bounds__(kPipeBlock) void bwd_q_pro(Params p, WalkCfg c) {
+  constexpr int VEC = VecOf<T>::value, esz = (int)sizeof(T);
+  WaveTile wt;
+  wave_tile<LPR>(p, c, wt);
+  const int h0 = wt.hg * (64 / LPR);
+  BwdQPro<T, LPR, NM, FAR> w;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) w.dw[e] = 0.f;
+  w.init(p, wt.li);
+  w.q = make_split(p.q, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.k = make_split(p.k, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.v = make_split(p.v, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.go = make_split(p.dout, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.dq = make_split(p.dq, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.lse = lse_stream(p, wt.b, h0, wt.hl);
+  w.tab = p.tab + ((int64_t)wt.b * p.T * p.H + h0 + wt.hl) * (2 * w.NS);
+  w.tst = (int64_t)p.H * 2 * w.NS;
+  w.scale = p.scale;
+  w.F = c.F;
+  w.a = wt.a;
+  w.end = min(wt.a + c.P, p.T);
+  // Queries a-2, a-1 only fill the near-source rotation (slot of u is
+  // (u - a + 2) & 3); the trip count depends only on P.
+  walk4(w, wt.a - 2, wt.a + c.P - 1);
+  write_wave_partial<T, LPR, true>(w.dw, p.dwq_part, pipe_wave_id(c), p.D);
+}
+
+template <typename T, int LPR, int NM, bool FAR>
+__global__ __launch_bounds__(kPipeBlock) void bwd_k_pro(Params p, WalkCfg c) {
+  constexpr int VEC = VecOf<T>::value, esz = (int)sizeof(T);
+  WaveTile wt;
+  wave_tile<LPR>(p, c, wt);
+  const int h0 = wt.hg * (64 / LPR);
+  BwdKPro<T, LPR, NM, FAR> w;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) w.dw[e] = 0.f;
+  w.init(p, wt.li);
+  w.q = make_split(p.q, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.k = make_split(p.k, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.go = make_split(p.dout, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.dk = make_split(p.dk, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.dv = make_split(p.dv, esz, wt.b, h0, wt.hl, wt.li, p.D, w.HV);
+  w.tab = p.tab + ((int64_t)wt.b * p.T * p.H + h0 + wt.hl) * (2 * w.NS);
+  w.tst = (int64_t)p.H * 2 * w.NS;
+  w.F = c.F;
+  w.a = wt.a;
+  w.end = min(wt.a + c.P, p.T);
+  w.T_ = p.T;
+  // Walk u = a .. a+P+1 (slot of u is (u - a) & 3); key u - 2 is finished at step u.
+  walk4(w, wt.a, wt.a + c.P + 1);
+  write_wave_partial<T, LPR, true>(w.dw, p.dwk_part, pipe_wave_id(c), p.D);
+}
+
+
+}  // namespace
+
+template <typename T, int LPR, int NM, bool FAR>
+hipError_t pro_pattern(bool fwd, const Params& p, const WalkCfg& c, hipStream_t st) {
+  const dim3 grid((unsigned)c.nwg), block(kPipeBlock);
+  if (fwd) {
+    hipLaunchKernelGGL((fwd_pipe_pro<T, LPR, NM, FAR>), grid, block, kPipeLds, st, p, c);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL((bwd_q_pro<T, LPR, NM, FAR>), grid, block, kPipeLds, st, p, c);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((bwd_k_pro<T, LPR, NM, FAR>), grid, block, kPipeLds, st, p, c);
+  return hipGetLastError();
+}
+
+hipError_t launch_pro(bool fwd, const Params& p, const WalkCfg& c, const Pattern& pat, int dtype,
+                      int lpr, hipStream_t st) {
+  return by_type_lpr(dtype, lpr, [&](auto tag, auto lprc) -> hipError_t {
+    using T = typename decltype(tag)::type;
+    constexpr int L = decltype(lprc)::value;
+    if (pat.far == 0) {
+      if (pat.nm == 3) return pro_pattern<T, L, 3, false>(fwd, p, c, st);
+      if (pat.nm == 5) return pro_pattern<T, L, 5, false>(fwd, p, c, st);
+    } else {
+      if (pat.nm == 7) return pro_pattern<T, L, 7, true>(fwd, p, c, st);
+      if (pat.nm == 1) return pro_pattern<T, L, 1, true>(fwd, p, c, st);
+    }
+    return hipErrorInvalidValue;
+  });
+}
+
+hipError_t launch_fwd_pro(const Params& p, const WalkCfg& c, const Pattern& pat, int dtype,
+                          int lpr, hipStream_t st) {
+  return launch_pro(true, p, c, pat, dtype, lpr, st);
+}
+
+hipError_t launch_bwd_pro(const Params& p, const WalkCfg& c, const Pattern& pat, int dtype,
+                          int lpr, hipStream_t st) {
+  return launch_pro(false, p, c, pat, dtype, lpr, st);
+}
+
+}  // namespace walk
+}  // namespace sbda

@@ -171,6 +171,11 @@ void walk_partials(const Params& p, int dtype, int64_t* pq, int64_t* pk, int64_t
   Pattern pat;
   classify(p, &pat);
   const WalkCfg c = launch_cfg(p, dtype, pat, walk_lpr(p, dtype), false, true);
+  if (pat.far == 0) {   // fused single-pass backward: no weight table
+    *pq = *pk = (int64_t)c.nwg * c.waves;
+    *tab_floats = 0;
+    return;
+  }
   *pq = (int64_t)c.nwg * c.waves;
   *pk = *pq;
   *tab_floats = (int64_t)p.B * p.T * p.H * 2 * p.S;

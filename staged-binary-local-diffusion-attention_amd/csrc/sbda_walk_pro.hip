@@ -25,6 +25,7 @@ namespace {
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+
 // Split-layout rows: a lane holds HV elements of each half (byte offsets
 // lo and hi inside a position), so RoPE partners share a lane.
 struct SplitStream {
@@ -527,20 +528,192 @@ __global__ __launch_bounds__(kPipeBlock) void bwd_k_pro(Params p, WalkCfg c) {
 }
 
 
+// ---- fused single-pass backward (far-free patterns)
+//
+// One walk per row as in the plain backward: each query's weights and score
+// gradients once, dQ through the transposed prologue at once, key j = u - 2
+// finalised from queries j, j + 1, j + 2 (roped q rows kept in registers),
+// then dK through the transposed prologue.  No weight table in global memory.
+// (A lockstep row-chain version for far offsets measured slower than the
+// two-pass backward -- 256 VGPRs with spills and five prologue applications
+// per step -- so far offsets keep the two passes.)
+
+
+template <typename T, int LPR, int NM>
+struct BwdFusedPro : ProBase<T, LPR> {
+  using B_ = ProBase<T, LPR>;
+  using B_::VEC;
+  using B_::HV;
+  using PL = typename B_::PL;
+  static constexpr int NN = NearSet<NM>::count;
+  static constexpr int NS = NN;
+
+  SplitStream q, k, v, go, dq, dk, dv;
+  Stream lse;
+  float scale;
+  int T_, a, end;
+  Raw kr[4], vr[4], gr[4];    // raw k (self slot and dK), v, dO rotations
+  Raw qr[2];                  // raw q of this step
+  float lr[2];
+  float kh[4][VEC];           // roped k rotation (near sources)
+  float qh[4][VEC];           // roped q rotation (near queries of a key)
+  float rk[4];                // k norm factors
+  float sp[4][3], sd[4][3];   // query's near-slot p_n and scale * dS_n
+  float dwq[VEC], dwk[VEC];
+
+  template <int R>
+  __device__ inline void prefetch(int u) {
+    const int uc = clampi(u, this->Tm1);
+    kr[R] = load_split<true>(k, uc);
+    vr[R] = load_split<true>(v, uc);
+    qr[R & 1] = load_split<true>(q, uc);
+    gr[R] = load_split<true>(go, uc);
+    lr[R & 1] = load_f32(lse, uc);
+  }
+
+  template <int R>
+  __device__ inline void compute(int u) {
+    float cu[HV], su[HV];
+    this->cs(clampi(u, this->Tm1), cu, su);
+    rk[R] = this->rope(kr[R], this->wk, cu, su, kh[R]);
+    float qx[VEC];
+    widen<T>(qr[R & 1], qx);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) qh[R][e] = qx[e];
+    const float rq = PL::forward_w(qh[R], this->wq, cu, su, this->D, this->eps);
+    {
+      const float* ks[NS];
+      const Raw* vs[NS];
+      bool ok[NS];
+      int idx = 0;
+#pragma unroll
+      for (int n = 0; n < 3; ++n) {
+        if (NM & (1 << n)) {
+          ks[idx] = kh[(R + 4 - n) & 3];
+          vs[idx] = &vr[(R + 4 - n) & 3];
+          ok[idx] = u - n >= 0;
+          ++idx;
+        }
+      }
+      float pp[NS], dp[NS], delta = 0.f;
+#pragma unroll
+      for (int s_ = 0; s_ < NS; ++s_) {
+        float a_ = 0.f;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) a_ = __builtin_fmaf(qh[R][e], ks[s_][e], a_);
+        const float sc = row_sum<LPR>(a_) * scale;
+        dp[s_] = row_sum<LPR>(dot_raw<T>(gr[R], *vs[s_]));
+        pp[s_] = ok[s_] ? fast_exp(sc - lr[R & 1]) : 0.f;
+        delta = __builtin_fmaf(pp[s_], dp[s_], delta);
+      }
+      float ds[NS];
+#pragma unroll
+      for (int s_ = 0; s_ < NS; ++s_) ds[s_] = pp[s_] * (dp[s_] - delta) * scale;
+#pragma unroll
+      for (int n = 0; n < NN; ++n) {
+        sp[R][n] = pp[n];
+        sd[R][n] = ds[n];
+      }
+      if (u >= a && u < end) {
+        float g[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) g[e] = 0.f;
+#pragma unroll
+        for (int s_ = 0; s_ < NS; ++s_) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) g[e] = __builtin_fmaf(ds[s_], ks[s_][e], g[e]);
+        }
+        PL::backward_w(g, qx, rq, this->wq, cu, su, this->D, dwq);
+        store_split<T>(dq, u, g);
+      }
+    }
+    // Key j = u - 2: near contributions from queries j + n, far from j + F.
+    const int j = u - 2;
+    if (j >= a && j < end) {
+      float ak[VEC], av[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) { ak[e] = 0.f; av[e] = 0.f; }
+      int idx = 0;
+#pragma unroll
+      for (int n = 0; n < 3; ++n) {
+        if (NM & (1 << n)) {
+          const int slot = (R + 2 + n) & 3;   // query j + n
+          const bool there = j + n < T_;
+          const float cs_ = there ? sd[slot][idx] : 0.f;
+          const float cp_ = there ? sp[slot][idx] : 0.f;
+          float gx[VEC];
+          widen<T>(gr[slot], gx);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            ak[e] = __builtin_fmaf(cs_, qh[slot][e], ak[e]);
+            av[e] = __builtin_fmaf(cp_, gx[e], av[e]);
+          }
+          ++idx;
+        }
+      }
+      float kx[VEC], cj[HV], sj[HV];
+      widen<T>(kr[(R + 2) & 3], kx);
+      this->cs(clampi(j, this->Tm1), cj, sj);
+      PL::backward_w(ak, kx, rk[(R + 2) & 3], this->wk, cj, sj, this->D, dwk);
+      store_split<T>(dk, j, ak);
+      store_split<T>(dv, j, av);
+    }
+  }
+};
+
+// Far-free patterns: lockstep 8-wave workgroups over consecutive tiles (the
+// same decode and trip counts as the other pipelined walks).
+template <typename T, int LPR, int NM>
+__global__ __launch_bounds__(kPipeBlock) void bwd_fused_pro(Params p, WalkCfg c) {
+  constexpr int VEC = VecOf<T>::value, esz = (int)sizeof(T);
+  WaveTile wt;
+  wave_tile<LPR>(p, c, wt);
+  const int h0 = wt.hg * (64 / LPR);
+  BwdFusedPro<T, LPR, NM> x;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    x.dwq[e] = 0.f;
+    x.dwk[e] = 0.f;
+  }
+  x.init(p, wt.li);
+  x.q = make_split(p.q, esz, wt.b, h0, wt.hl, wt.li, p.D, x.HV);
+  x.k = make_split(p.k, esz, wt.b, h0, wt.hl, wt.li, p.D, x.HV);
+  x.v = make_split(p.v, esz, wt.b, h0, wt.hl, wt.li, p.D, x.HV);
+  x.go = make_split(p.dout, esz, wt.b, h0, wt.hl, wt.li, p.D, x.HV);
+  x.dq = make_split(p.dq, esz, wt.b, h0, wt.hl, wt.li, p.D, x.HV);
+  x.dk = make_split(p.dk, esz, wt.b, h0, wt.hl, wt.li, p.D, x.HV);
+  x.dv = make_split(p.dv, esz, wt.b, h0, wt.hl, wt.li, p.D, x.HV);
+  x.lse = lse_stream(p, wt.b, h0, wt.hl);
+  x.scale = p.scale;
+  x.T_ = p.T;
+  x.a = wt.a;
+  x.end = min(wt.a + c.P, p.T);
+  // u = a-2 .. a+P+1 (slot of u is (u - a + 2) & 3); the trip count depends only on P.
+  walk4(x, wt.a - 2, wt.a + c.P + 1);
+  const int64_t wave = pipe_wave_id(c);
+  write_wave_partial<T, LPR, true>(x.dwq, p.dwq_part, wave, p.D);
+  write_wave_partial<T, LPR, true>(x.dwk, p.dwk_part, wave, p.D);
+}
+
 }  // namespace
 
 template <typename T, int LPR, int NM, bool FAR>
-hipError_t pro_pattern(bool fwd, const Params& p, const WalkCfg& c, hipStream_t st) {
+hipError_t pro_pattern(bool fwd, const Params& p, const WalkCfg& c, int dtype, hipStream_t st) {
   const dim3 grid((unsigned)c.nwg), block(kPipeBlock);
   if (fwd) {
     hipLaunchKernelGGL((fwd_pipe_pro<T, LPR, NM, FAR>), grid, block, kPipeLds, st, p, c);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL((bwd_q_pro<T, LPR, NM, FAR>), grid, block, kPipeLds, st, p, c);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((bwd_k_pro<T, LPR, NM, FAR>), grid, block, kPipeLds, st, p, c);
-  return hipGetLastError();
+  if constexpr (!FAR) {
+    hipLaunchKernelGGL((bwd_fused_pro<T, LPR, NM>), grid, block, kPipeLds, st, p, c);
+    return hipGetLastError();
+  } else {
+    hipLaunchKernelGGL((bwd_q_pro<T, LPR, NM, FAR>), grid, block, kPipeLds, st, p, c);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((bwd_k_pro<T, LPR, NM, FAR>), grid, block, kPipeLds, st, p, c);
+    return hipGetLastError();
+  }
 }
 
 hipError_t launch_pro(bool fwd, const Params& p, const WalkCfg& c, const Pattern& pat, int dtype,
@@ -549,11 +722,11 @@ hipError_t launch_pro(bool fwd, const Params& p, const WalkCfg& c, const Pattern
     using T = typename decltype(tag)::type;
     constexpr int L = decltype(lprc)::value;
     if (pat.far == 0) {
-      if (pat.nm == 3) return pro_pattern<T, L, 3, false>(fwd, p, c, st);
-      if (pat.nm == 5) return pro_pattern<T, L, 5, false>(fwd, p, c, st);
+      if (pat.nm == 3) return pro_pattern<T, L, 3, false>(fwd, p, c, dtype, st);
+      if (pat.nm == 5) return pro_pattern<T, L, 5, false>(fwd, p, c, dtype, st);
     } else {
-      if (pat.nm == 7) return pro_pattern<T, L, 7, true>(fwd, p, c, st);
-      if (pat.nm == 1) return pro_pattern<T, L, 1, true>(fwd, p, c, st);
+      if (pat.nm == 7) return pro_pattern<T, L, 7, true>(fwd, p, c, dtype, st);
+      if (pat.nm == 1) return pro_pattern<T, L, 1, true>(fwd, p, c, dtype, st);
     }
     return hipErrorInvalidValue;
   });

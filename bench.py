@@ -70,8 +70,9 @@ def cpu_baseline(layers: int, h: int, d: int, seconds_target: float = 15.0) -> d
 
     t = 4096
     elapsed = run(t)
-    # Grow the sample until one 20-layer pass takes a sizeable share of the target.
-    while elapsed < seconds_target / 4 and t < (1 << 20):
+    # Grow the sample until one 20-layer pass takes at least half the target
+    # (about 10-15 s of CPU work in all, counting the smaller passes).
+    while elapsed < seconds_target / 2 and t < (1 << 20):
         t *= 2
         elapsed = run(t)
     model = ""

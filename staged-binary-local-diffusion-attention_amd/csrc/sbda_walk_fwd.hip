@@ -94,7 +94,8 @@ struct FwdPipe {
 #pragma unroll
       for (int e = 0; e < VEC; ++e) acc[e] = __builtin_fmaf(w[NS - 1], vf[e], acc[e]);
     }
-    const float inv = l > 0.f ? 1.f / l : 0.f;
+    // l >= 1 whenever a source is valid (the largest term is exp(0)).
+    const float inv = l > 0.f ? __builtin_amdgcn_rcpf(l) : 0.f;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[e] *= inv;
     if (store) {

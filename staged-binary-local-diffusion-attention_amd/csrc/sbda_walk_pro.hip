@@ -81,14 +81,16 @@ struct ProBase {
   static constexpr int VEC = VecOf<T>::value;
   static constexpr int HV = VEC / 2;
   using PL = Prologue<T, LPR>;
+  // A walk row is LPR lanes of 16 bytes, so the head dimension is a
+  // compile-time power of two and the norm's mean is an exact scaling.
+  static constexpr int D = 16 * LPR / (int)sizeof(T);
   Stream rc, rs;   // fp32 [T, D/2] RoPE tables: this lane's HV entries of a position
   float eps;
-  int li, D, Tm1;
+  int li, Tm1;
   float wq[VEC], wk[VEC];
 
   __device__ inline void init(const Params& p, int lane_in_row) {
     li = lane_in_row;
-    D = p.D;
     Tm1 = p.T - 1;
     eps = p.eps;
     const int half = D >> 1;
@@ -205,7 +207,8 @@ struct FwdPipePro : ProBase<T, LPR> {
 #pragma unroll
       for (int e = 0; e < VEC; ++e) acc[e] = __builtin_fmaf(w[NS - 1], vf[e], acc[e]);
     }
-    const float inv = l > 0.f ? 1.f / l : 0.f;
+    // l >= 1 whenever a source is valid (the largest term is exp(0)).
+    const float inv = l > 0.f ? __builtin_amdgcn_rcpf(l) : 0.f;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[e] *= inv;
     if (store) {

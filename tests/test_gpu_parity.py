@@ -227,6 +227,43 @@ def test_prologue_matches_oracle(dtype, tol, layer):
         assert (a - w).abs().max().item() / scale < (2e-2 if dtype != torch.float32 else 1e-4), name
 
 
+@pytest.mark.parametrize("dtype,h,d", [(torch.bfloat16, 16, 32), (torch.bfloat16, 4, 128),
+                                       (torch.float16, 8, 64), (torch.float32, 8, 32),
+                                       (torch.float32, 16, 16)])
+@pytest.mark.parametrize("layer", [1, 3, 9])
+def test_prologue_across_head_dims(dtype, h, d, layer):
+    # Rows of 4, 8 and 16 lanes in the prologue walks (the head dimension is
+    # a compile-time function of the lane count there), far-free and far.
+    theta = 10000.0
+    b, t = 1, 3000
+    q, k, v, g = _inputs(b, t, h, d, dtype, seed=900 + layer + d)
+    gen = torch.Generator().manual_seed(901 + d)
+    wq = (1 + 0.1 * torch.randn(d, generator=gen))
+    wk = (1 + 0.1 * torch.randn(d, generator=gen))
+    offs = ref.sbda_layer_offsets(layer)
+    qd, kd, vd = (_dev(x).requires_grad_() for x in (q, k, v))
+    wqd, wkd = wq.to(DEV).requires_grad_(), wk.to(DEV).requires_grad_()
+    out = sbda_amd.fused_sbda_prologue(qd, kd, vd, torch.tensor(offs, dtype=torch.int32, device=DEV),
+                                       wqd, wkd, theta=theta)
+    out.backward(_dev(g))
+    torch.cuda.synchronize()
+    rq, rk, rv = (x.float().requires_grad_() for x in (q, k, v))
+    rwq, rwk = wq.clone().requires_grad_(), wk.clone().requires_grad_()
+    qq, kk = ref.prologue(rq, rk, rwq, rwk, theta)
+    want = ref.gather_attention(qq.permute(0, 2, 1, 3), kk.permute(0, 2, 1, 3), rv.permute(0, 2, 1, 3), offs)
+    want.backward(g.float().permute(0, 2, 1, 3))
+    tol = dict(rtol=1e-4, atol=1e-5) if dtype == torch.float32 else LOW_TOL
+    pairs = [("out", out, want), ("dq", qd.grad, rq.grad.permute(0, 2, 1, 3)),
+             ("dk", kd.grad, rk.grad.permute(0, 2, 1, 3)), ("dv", vd.grad, rv.grad.permute(0, 2, 1, 3))]
+    for name, a, w in pairs:
+        torch.testing.assert_close(a.detach().float().cpu(), w.detach(), **tol,
+                                   msg=lambda m: f"prologue {name} ({dtype}, h={h}, d={d}): {m}")
+    for name, a, w in (("dwq", wqd.grad, rwq.grad), ("dwk", wkd.grad, rwk.grad)):
+        a = a.float().cpu()
+        scale = w.abs().max().item() + 1e-6
+        assert (a - w).abs().max().item() / scale < (2e-2 if dtype != torch.float32 else 1e-4), name
+
+
 # --------------------------------------------------- metric-size properties
 
 @pytest.mark.parametrize("layer", [3, 20])

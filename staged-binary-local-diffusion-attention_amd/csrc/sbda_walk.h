@@ -77,6 +77,55 @@ struct WalkCfg {
   int64_t total; // tiles in the grid
 };
 
+// Row chains (column order, F a multiple of P): a workgroup of W waves walks
+// W consecutive rows of F positions (t = r * F + c) over one column band in
+// lockstep, so each wave's far rows are its neighbours' own rows.
+struct ChainCfg {
+  int P, F, rows, W, bands;
+  int L;        // rows per chain; a workgroup holds W / L chains on adjacent bands
+  int blocks;   // row blocks (ceil(rows / L)) per band
+  int bgroups;  // band groups (ceil(bands / (W / L)))
+  int HG, nwg;
+};
+
+// W = 8 rows (fewer when the sequence has fewer rows), at most 4 when rows
+// are 32 MiB or more apart: eight lockstep waves on addresses that far apart
+// collide in the DRAM channel mapping.  One chain per workgroup (L = W):
+// shorter chains on more bands measured slower.
+inline ChainCfg make_chain_cfg(int64_t B, int64_t row_stride_bytes, const WalkCfg& wc) {
+  ChainCfg c{};
+  c.P = wc.P;
+  c.F = wc.F;
+  c.rows = wc.rows;
+  c.W = c.rows >= 8 ? 8 : c.rows >= 4 ? 4 : c.rows >= 2 ? 2 : 1;
+  if ((int64_t)wc.F * row_stride_bytes >= kBigStride && c.W > 4) c.W = 4;
+  c.L = c.W;
+  c.bands = wc.F / wc.P;
+  c.blocks = (c.rows + c.L - 1) / c.L;
+  c.bgroups = (c.bands + c.W / c.L - 1) / (c.W / c.L);
+  c.HG = wc.HG;
+  const int64_t nwg = B * c.HG * c.bgroups * c.blocks;
+  c.nwg = (nwg <= 0 || nwg > 0x7fffffff) ? 0 : (int)nwg;
+  return c;
+}
+
+// Chained prologue backward (far F >= 16): the keys of a chain's last row
+// whose far query lies in the next chain are finished by a second kernel
+// from a workspace of deferred slots, one per (batch, head group, row block,
+// column): the key's near-slot dK' and dV rows (fp32, 64 / LPR heads x D
+// each) and the far query's weight pair per head.
+constexpr int kFixCols = 8;   // deferred columns per finishing wave
+
+__host__ __device__ inline int64_t chain_pro_slots(int64_t B, const ChainCfg& c) {
+  return B * c.HG * c.blocks * c.F;
+}
+__host__ __device__ inline int64_t chain_pro_slot_floats(int lpr, int D) {
+  return 2 * (64 / lpr) * (int64_t)D;
+}
+__host__ __device__ inline int64_t chain_pro_fix_waves(int64_t B, const ChainCfg& c) {
+  return B * c.HG * c.blocks * ((c.F + kFixCols - 1) / kFixCols);
+}
+
 // Workgroups are dealt to the 8 XCDs round-robin; give each XCD a contiguous
 // range of tiles instead.
 __device__ inline int64_t xcd_remap(int wg, int nwg) {

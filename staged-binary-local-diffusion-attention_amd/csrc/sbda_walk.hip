@@ -176,6 +176,16 @@ void walk_partials(const Params& p, int dtype, int64_t* pq, int64_t* pk, int64_t
     *tab_floats = 0;
     return;
   }
+  if (c.column) {   // chained backward + finishing kernel (sbda_walk_pro.hip)
+    const int lpr = walk_lpr(p, dtype);
+    const int esz = dtype == kFP32 ? 4 : 2;
+    const walk::ChainCfg cc = walk::make_chain_cfg(p.B, p.q.st * (int64_t)esz, c);
+    const int64_t slots = walk::chain_pro_slots(p.B, cc);
+    *pq = (int64_t)cc.nwg * cc.W;
+    *pk = *pq + 4 * ((walk::chain_pro_fix_waves(p.B, cc) + 3) / 4);
+    *tab_floats = slots * (walk::chain_pro_slot_floats(lpr, p.D) + 2 * (64 / lpr));
+    return;
+  }
   *pq = (int64_t)c.nwg * c.waves;
   *pk = *pq;
   *tab_floats = (int64_t)p.B * p.T * p.H * 2 * p.S;

@@ -237,14 +237,6 @@ struct ChainSlot {
   float2 pd[kChainRing][64];      // [u & 3][lane]: (p_far, scale * dS_far) of query u
 };
 
-struct ChainCfg {
-  int P, F, rows, W, bands;
-  int L;        // rows per chain; a workgroup holds W / L chains on adjacent bands
-  int blocks;   // row blocks (ceil(rows / L)) per band
-  int bgroups;  // band groups (ceil(bands / (W / L)))
-  int HG, nwg;
-};
-
 template <typename T, int LPR, int NM, bool LEFT_LDS, bool RIGHT_LDS>
 struct BwdChain {
   static constexpr int VEC = VecOf<T>::value;
@@ -772,23 +764,8 @@ __global__ __launch_bounds__(64 * F) void bwd_tc(Params p, TcCfg cfg) {
 
 template <typename T, int LPR, int NM>
 hipError_t launch_chain(const Params& p, const WalkCfg& wc, hipStream_t st) {
-  ChainCfg c{};
-  c.P = wc.P;
-  c.F = wc.F;
-  c.rows = wc.rows;
-  c.W = c.rows >= 8 ? 8 : c.rows >= 4 ? 4 : c.rows >= 2 ? 2 : 1;
-  // Same DRAM-channel limit as the forward's row groups (walk_launch).
-  if ((int64_t)wc.F * p.q.st * (int64_t)sizeof(T) >= kBigStride && c.W > 4) c.W = 4;
-  // One chain per workgroup (L = W): shorter chains on more bands measured
-  // slower (backward 30.7 -> 32.0 ms per step at L = 4).
-  c.L = c.W;
-  c.bands = wc.F / wc.P;
-  c.blocks = (c.rows + c.L - 1) / c.L;
-  c.bgroups = (c.bands + c.W / c.L - 1) / (c.W / c.L);
-  c.HG = wc.HG;
-  const int64_t nwg = (int64_t)p.B * c.HG * c.bgroups * c.blocks;
-  if (nwg <= 0 || nwg > 0x7fffffff) return hipErrorInvalidValue;
-  c.nwg = (int)nwg;
+  const ChainCfg c = make_chain_cfg(p.B, p.q.st * (int64_t)sizeof(T), wc);
+  if (c.nwg <= 0) return hipErrorInvalidValue;
   const dim3 grid((unsigned)c.nwg), block(64 * c.W);
   switch (c.W) {
     case 8: hipLaunchKernelGGL((bwd_chain<T, LPR, NM, 8>), grid, block, 0, st, p, c); break;

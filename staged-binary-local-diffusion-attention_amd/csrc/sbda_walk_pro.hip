@@ -698,6 +698,411 @@ __global__ __launch_bounds__(kPipeBlock) void bwd_fused_pro(Params p, WalkCfg c)
   write_wave_partial<T, LPR, true>(x.dwk, p.dwk_part, wave, p.D);
 }
 
+// ===================================== chained backward, fused prologue (F >= 16)
+//
+// Far offsets F >= 16 that tile the sequence into rows (t = r * F + c): a
+// workgroup of W waves walks W consecutive rows of one column band in
+// lockstep, one barrier per step, as the plain chained backward does, and
+// every raw q/k row gets the prologue once, when it arrives.  Wave w
+// publishes in LDS its roped k and raw v rows (wave w + 1's far-left sources,
+// read in the same step) and its roped q, raw dO and far-slot weights
+// (wave w - 1's far-key contribution, read two steps later).  The first wave
+// of a chain loads and ropes its far-left rows.  The keys of the last wave
+// whose far query lies in the next chain's first row are finished by
+// bwd_fix_pro: the last wave stores their near-slot dK' and dV (fp32, before
+// the transposed prologue), the next chain's first wave stores those far
+// queries' weight pairs, and bwd_fix_pro adds the far term and applies the
+// transposed prologue -- the same sums in the same order as a key finished in
+// one pass.  Every wave runs the same trip count (rows past the end walk
+// clamped rows and store nothing), so all barriers are reached.
+
+constexpr int kProRing = 4;   // q/dO/weight ring: written at step u, read at u + 2
+
+template <int VEC>
+struct ChainProSlot {
+  float4 kf[2][VEC / 4][64];         // [u & 1][quarter][lane]: roped k of position u
+  u32x4 vf[2][64];                   // [u & 1][lane]: raw v
+  float4 qf[kProRing][VEC / 4][64];  // [u & 3][quarter][lane]: roped q
+  u32x4 gf[kProRing][64];            // [u & 3][lane]: raw dO
+  float2 pc[kProRing][16];           // [u & 3][head]: (p_far, scale * dS_far) of query u
+};
+
+__device__ inline u32x4 pack_raw(const Raw& r) { return u32x4{r.w[0], r.w[1], r.w[2], r.w[3]}; }
+__device__ inline Raw unpack_raw(const u32x4& x) { return Raw{{x.x, x.y, x.z, x.w}}; }
+
+template <int VEC>
+__device__ inline void put_rows(float4 (&dst)[VEC / 4][64], int lane, const float (&x)[VEC]) {
+#pragma unroll
+  for (int i = 0; i < VEC / 4; ++i)
+    dst[i][lane] = make_float4(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+}
+
+template <int VEC>
+__device__ inline void get_rows(const float4 (&src)[VEC / 4][64], int lane, float (&x)[VEC]) {
+#pragma unroll
+  for (int i = 0; i < VEC / 4; ++i) {
+    const float4 v = src[i][lane];
+    x[4 * i] = v.x;
+    x[4 * i + 1] = v.y;
+    x[4 * i + 2] = v.z;
+    x[4 * i + 3] = v.w;
+  }
+}
+
+template <typename T, int LPR, int NM, bool LEFT_LDS, bool RIGHT_LDS>
+struct BwdChainPro : ProBase<T, LPR> {
+  using B_ = ProBase<T, LPR>;
+  using B_::VEC;
+  using B_::HV;
+  using PL = typename B_::PL;
+  using Slot = ChainProSlot<VecOf<T>::value>;
+  static constexpr int NN = NearSet<NM>::count;
+  static constexpr int NS = NN + 1;
+
+  SplitStream q, k, v, go, dq, dk, dv;
+  Stream lse;
+  float scale;
+  int F, T_, a, end, lane, hl;
+  Slot* mine;
+  const Slot* up;      // wave w - 1 (far-left provider)
+  const Slot* down;    // wave w + 1 (far-right provider)
+  float4* defer;       // last wave: deferred dK'/dV slots of its band's columns
+  float2* defer_pc;    // first wave: far weight pairs of the previous chain's deferred keys
+  Raw kr[4], vr[4], gr[4];
+  Raw qr[2];
+  float lr[2];
+  Raw kl[2], vl[2];            // far-left raw rows of query u (first wave)
+  float clc[2][HV], cls[2][HV];
+  float kh[4][VEC];            // roped k rotation
+  float qh[4][VEC];            // roped q rotation
+  float rk[4];
+  float sp[4][3], sd[4][3];
+  float dwq[VEC], dwk[VEC];
+
+  template <int R>
+  __device__ inline void prefetch(int u) {
+    const int uc = clampi(u, this->Tm1);
+    kr[R] = load_split(k, uc);
+    vr[R] = load_split(v, uc);
+    qr[R & 1] = load_split(q, uc);
+    gr[R] = load_split(go, uc);
+    lr[R & 1] = load_f32(lse, uc);
+    if constexpr (!LEFT_LDS) {
+      const int ul = clampi(u - F, this->Tm1);
+      kl[R & 1] = load_split(k, ul);
+      vl[R & 1] = load_split(v, ul);
+      this->cs(ul, clc[R & 1], cls[R & 1]);
+    }
+  }
+
+  // dK' -> dK through the transposed prologue, then both rows out.
+  template <int R>
+  __device__ inline void finish_key(int j, float (&ak)[VEC], const float (&av)[VEC]) {
+    float kx[VEC], cj[HV], sj[HV];
+    widen<T>(kr[(R + 2) & 3], kx);
+    this->cs(clampi(j, this->Tm1), cj, sj);
+    PL::backward_w(ak, kx, rk[(R + 2) & 3], this->wk, cj, sj, this->D, dwk);
+    store_split<T>(dk, j, ak);
+    store_split<T>(dv, j, av);
+  }
+
+  template <int R>
+  __device__ inline void compute(int u) {
+    float cu[HV], su[HV];
+    this->cs(clampi(u, this->Tm1), cu, su);
+    rk[R] = this->rope(kr[R], this->wk, cu, su, kh[R]);
+    float qx[VEC];
+    widen<T>(qr[R & 1], qx);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) qh[R][e] = qx[e];
+    const float rq = PL::forward_w(qh[R], this->wq, cu, su, this->D, this->eps);
+    // Publish this step's rows, then wait for the neighbours'.
+    put_rows<VEC>(mine->kf[R & 1], lane, kh[R]);
+    mine->vf[R & 1][lane] = pack_raw(vr[R]);
+    put_rows<VEC>(mine->qf[R], lane, qh[R]);
+    mine->gf[R][lane] = pack_raw(gr[R]);
+    __syncthreads();
+    float kfar[VEC];
+    Raw vfar;
+    if constexpr (LEFT_LDS) {
+      get_rows<VEC>(up->kf[R & 1], lane, kfar);
+      vfar = unpack_raw(up->vf[R & 1][lane]);
+    } else {
+      this->rope(kl[R & 1], this->wk, clc[R & 1], cls[R & 1], kfar);
+      vfar = vl[R & 1];
+    }
+    {
+      const float* ks[NS];
+      const Raw* vs[NS];
+      bool ok[NS];
+      int idx = 0;
+#pragma unroll
+      for (int n = 0; n < 3; ++n) {
+        if (NM & (1 << n)) {
+          ks[idx] = kh[(R + 4 - n) & 3];
+          vs[idx] = &vr[(R + 4 - n) & 3];
+          ok[idx] = u - n >= 0;
+          ++idx;
+        }
+      }
+      ks[NS - 1] = kfar;
+      vs[NS - 1] = &vfar;
+      ok[NS - 1] = u - F >= 0;
+      float pp[NS], dp[NS], delta = 0.f;
+#pragma unroll
+      for (int s_ = 0; s_ < NS; ++s_) {
+        float a_ = 0.f;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) a_ = __builtin_fmaf(qh[R][e], ks[s_][e], a_);
+        const float sc = row_sum<LPR>(a_) * scale;
+        dp[s_] = row_sum<LPR>(dot_raw<T>(gr[R], *vs[s_]));
+        pp[s_] = ok[s_] ? fast_exp(sc - lr[R & 1]) : 0.f;
+        delta = __builtin_fmaf(pp[s_], dp[s_], delta);
+      }
+      float ds[NS];
+#pragma unroll
+      for (int s_ = 0; s_ < NS; ++s_) ds[s_] = pp[s_] * (dp[s_] - delta) * scale;
+#pragma unroll
+      for (int n = 0; n < NN; ++n) {
+        sp[R][n] = pp[n];
+        sd[R][n] = ds[n];
+      }
+      const float2 far_w = make_float2(pp[NS - 1], ds[NS - 1]);
+      if (this->li == 0) mine->pc[R][hl] = far_w;
+      if constexpr (!LEFT_LDS) {
+        if (defer_pc != nullptr && u >= a && u < end && this->li == 0)
+          defer_pc[(int64_t)(u - a) * (64 / LPR) + hl] = far_w;
+      }
+      if (u >= a && u < end) {
+        float g[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) g[e] = 0.f;
+#pragma unroll
+        for (int s_ = 0; s_ < NS; ++s_) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) g[e] = __builtin_fmaf(ds[s_], ks[s_][e], g[e]);
+        }
+        PL::backward_w(g, qx, rq, this->wq, cu, su, this->D, dwq);
+        store_split<T>(dq, u, g);
+      }
+    }
+    // Key j = u - 2: near contributions from queries j + n, far from j + F.
+    const int j = u - 2;
+    if (j >= a && j < end) {
+      float ak[VEC], av[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) { ak[e] = 0.f; av[e] = 0.f; }
+      int idx = 0;
+#pragma unroll
+      for (int n = 0; n < 3; ++n) {
+        if (NM & (1 << n)) {
+          const int slot = (R + 2 + n) & 3;   // query j + n
+          const bool there = j + n < T_;
+          const float cs_ = there ? sd[slot][idx] : 0.f;
+          const float cp_ = there ? sp[slot][idx] : 0.f;
+          float gx[VEC];
+          widen<T>(gr[slot], gx);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            ak[e] = __builtin_fmaf(cs_, qh[slot][e], ak[e]);
+            av[e] = __builtin_fmaf(cp_, gx[e], av[e]);
+          }
+          ++idx;
+        }
+      }
+      const bool there = j + F < T_;
+      if constexpr (RIGHT_LDS) {
+        // Query j + F is wave w + 1's query of step u - 2.
+        const int sl = (R + 2) & 3;
+        const float2 w2 = down->pc[sl][hl];
+        float qf[VEC], gx[VEC];
+        get_rows<VEC>(down->qf[sl], lane, qf);
+        widen<T>(unpack_raw(down->gf[sl][lane]), gx);
+        const float cs_ = there ? w2.y : 0.f;
+        const float cp_ = there ? w2.x : 0.f;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          ak[e] = __builtin_fmaf(cs_, qf[e], ak[e]);
+          av[e] = __builtin_fmaf(cp_, gx[e], av[e]);
+        }
+        finish_key<R>(j, ak, av);
+      } else {
+        if (there) {
+          // Far query in the next chain: bwd_fix_pro finishes this key.
+          float4* slot = defer + (int64_t)(j - a) * (2 * (VEC / 4) * 64);
+#pragma unroll
+          for (int i = 0; i < VEC / 4; ++i) {
+            slot[i * 64 + lane] = make_float4(ak[4 * i], ak[4 * i + 1], ak[4 * i + 2], ak[4 * i + 3]);
+            slot[(VEC / 4 + i) * 64 + lane] =
+                make_float4(av[4 * i], av[4 * i + 1], av[4 * i + 2], av[4 * i + 3]);
+          }
+        } else {
+          finish_key<R>(j, ak, av);
+        }
+      }
+    }
+  }
+
+  __device__ inline void walk(int u0, int end_u) {
+    // u = a-2 .. a+P+1 for every wave of the workgroup (same trip count).
+    this->template prefetch<0>(u0);
+    for (int u = u0; u <= end_u; u += 4) {
+      this->template prefetch<1>(u + 1);
+      this->template compute<0>(u);
+      this->template prefetch<2>(u + 2);
+      this->template compute<1>(u + 1);
+      this->template prefetch<3>(u + 3);
+      this->template compute<2>(u + 2);
+      this->template prefetch<0>(u + 4);
+      this->template compute<3>(u + 3);
+    }
+  }
+};
+
+template <typename T, int LPR, int NM, bool LEFT_LDS, bool RIGHT_LDS, int W>
+__device__ inline void chain_pro_wave(const Params& p, const ChainCfg& c,
+                                      ChainProSlot<VecOf<T>::value>* lds, int w, int b, int hg,
+                                      int rb, int cb, int a, int64_t wave) {
+  constexpr int VEC = VecOf<T>::value, esz = (int)sizeof(T);
+  const int lane = threadIdx.x & 63, hl = lane / LPR, li = lane % LPR;
+  const int h0 = hg * (64 / LPR);
+  BwdChainPro<T, LPR, NM, LEFT_LDS, RIGHT_LDS> x;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    x.dwq[e] = 0.f;
+    x.dwk[e] = 0.f;
+  }
+  x.init(p, li);
+  x.q = make_split(p.q, esz, b, h0, hl, li, p.D, x.HV);
+  x.k = make_split(p.k, esz, b, h0, hl, li, p.D, x.HV);
+  x.v = make_split(p.v, esz, b, h0, hl, li, p.D, x.HV);
+  x.go = make_split(p.dout, esz, b, h0, hl, li, p.D, x.HV);
+  x.dq = make_split(p.dq, esz, b, h0, hl, li, p.D, x.HV);
+  x.dk = make_split(p.dk, esz, b, h0, hl, li, p.D, x.HV);
+  x.dv = make_split(p.dv, esz, b, h0, hl, li, p.D, x.HV);
+  x.lse = lse_stream(p, b, h0, hl);
+  x.scale = p.scale;
+  x.F = c.F;
+  x.T_ = p.T;
+  x.a = a;
+  x.end = min(a + c.P, p.T);   // < a for a row past the end: nothing is stored
+  x.lane = lane;
+  x.hl = hl;
+  x.mine = lds + w;
+  x.up = lds + (LEFT_LDS ? w - 1 : w);
+  x.down = lds + (RIGHT_LDS ? w + 1 : w);
+  // Deferred slots: index ((b * HG + hg) * blocks + row block) * F + column.
+  const int64_t slots = chain_pro_slots(p.B, c);
+  const int64_t slot0 = (((int64_t)b * c.HG + hg) * c.blocks + rb) * c.F + (int64_t)cb * c.P;
+  x.defer = reinterpret_cast<float4*>(p.tab) + slot0 * (2 * (VEC / 4) * 64);
+  float2* pcs = reinterpret_cast<float2*>(p.tab + slots * chain_pro_slot_floats(LPR, p.D));
+  x.defer_pc = (!LEFT_LDS && rb > 0) ? pcs + (slot0 - c.F) * (64 / LPR) : nullptr;
+  x.walk(a - 2, a + c.P + 1);
+  write_wave_partial<T, LPR, true>(x.dwq, p.dwq_part, wave, p.D);
+  write_wave_partial<T, LPR, true>(x.dwk, p.dwk_part, wave, p.D);
+}
+
+template <typename T, int LPR, int NM, int W>
+__global__ __launch_bounds__(64 * W) void bwd_chain_pro(Params p, ChainCfg c) {
+  __shared__ ChainProSlot<VecOf<T>::value> lds[W];
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  // Workgroup -> (batch, head group, band, row block), XCD-contiguous; wave w
+  // -> row w of the block (one chain per workgroup).
+  int64_t g = xcd_remap(blockIdx.x, gridDim.x);
+  const int rb = (int)(g % c.blocks);
+  g /= c.blocks;
+  const int cb = (int)(g % c.bands);
+  g /= c.bands;
+  const int hg = (int)(g % c.HG);
+  const int b = (int)(g / c.HG);
+  const int r = rb * W + w;
+  const int64_t a64 = (int64_t)r * c.F + (int64_t)cb * c.P;
+  const int a = (r < c.rows && a64 < p.T) ? (int)a64 : p.T;
+  const int64_t wave = (int64_t)blockIdx.x * W + w;
+  if constexpr (W == 1) {
+    chain_pro_wave<T, LPR, NM, false, false, W>(p, c, lds, w, b, hg, rb, cb, a, wave);
+  } else {
+    if (w == 0)
+      chain_pro_wave<T, LPR, NM, false, true, W>(p, c, lds, w, b, hg, rb, cb, a, wave);
+    else if (w == W - 1)
+      chain_pro_wave<T, LPR, NM, true, false, W>(p, c, lds, w, b, hg, rb, cb, a, wave);
+    else
+      chain_pro_wave<T, LPR, NM, true, true, W>(p, c, lds, w, b, hg, rb, cb, a, wave);
+  }
+}
+
+// Finishes the deferred keys: the last row of every chain (row rb * W + W - 1)
+// whose far query j + F exists.  One wave per kFixCols columns of a row, no
+// barriers.  dK' = near part + c * roped q_{j+F}, dV = near part + p * dO_{j+F},
+// then the transposed prologue as in the chained walk.
+template <typename T, int LPR>
+__global__ __launch_bounds__(256) void bwd_fix_pro(Params p, ChainCfg c, int64_t part0) {
+  constexpr int VEC = VecOf<T>::value, HV = VEC / 2, esz = (int)sizeof(T);
+  using PL = Prologue<T, LPR>;
+  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int chunks = (c.F + kFixCols - 1) / kFixCols;
+  const int64_t nwaves = chain_pro_fix_waves(p.B, c);
+  float dwk[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) dwk[e] = 0.f;
+  if (wave < nwaves) {
+    int64_t g = wave;
+    const int chunk = (int)(g % chunks);
+    g /= chunks;
+    const int rb = (int)(g % c.blocks);
+    g /= c.blocks;
+    const int hg = (int)(g % c.HG);
+    const int b = (int)(g / c.HG);
+    const int r = rb * c.W + c.W - 1;
+    const int lane = threadIdx.x & 63, hl = lane / LPR, li = lane % LPR;
+    const int h0 = hg * (64 / LPR);
+    ProBase<T, LPR> pb;
+    pb.init(p, li);
+    const SplitStream q = make_split(p.q, esz, b, h0, hl, li, p.D, HV);
+    const SplitStream k = make_split(p.k, esz, b, h0, hl, li, p.D, HV);
+    const SplitStream go = make_split(p.dout, esz, b, h0, hl, li, p.D, HV);
+    const SplitStream dk = make_split(p.dk, esz, b, h0, hl, li, p.D, HV);
+    const SplitStream dv = make_split(p.dv, esz, b, h0, hl, li, p.D, HV);
+    const int64_t slots = chain_pro_slots(p.B, c);
+    const float4* rows = reinterpret_cast<const float4*>(p.tab);
+    const float2* pcs = reinterpret_cast<const float2*>(p.tab + slots * chain_pro_slot_floats(LPR, p.D));
+    const int c0 = chunk * kFixCols, c1 = min(c.F, c0 + kFixCols);
+    for (int col = c0; col < c1; ++col) {
+      const int64_t j64 = (int64_t)r * c.F + col;
+      if (c.W < 2 || r >= c.rows || j64 + c.F >= p.T) continue;
+      const int j = (int)j64, i = j + c.F;
+      const int64_t slot = (((int64_t)b * c.HG + hg) * c.blocks + rb) * c.F + col;
+      const float4* sr = rows + slot * (2 * (VEC / 4) * 64);
+      float ak[VEC], av[VEC];
+#pragma unroll
+      for (int n = 0; n < VEC / 4; ++n) {
+        const float4 x = sr[n * 64 + lane];
+        const float4 y = sr[(VEC / 4 + n) * 64 + lane];
+        ak[4 * n] = x.x; ak[4 * n + 1] = x.y; ak[4 * n + 2] = x.z; ak[4 * n + 3] = x.w;
+        av[4 * n] = y.x; av[4 * n + 1] = y.y; av[4 * n + 2] = y.z; av[4 * n + 3] = y.w;
+      }
+      const float2 w2 = pcs[slot * (64 / LPR) + hl];
+      float ci[HV], si[HV], qi[VEC], gx[VEC];
+      pb.cs(i, ci, si);
+      pb.rope(load_split(q, i), pb.wq, ci, si, qi);
+      widen<T>(load_split(go, i), gx);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        ak[e] = __builtin_fmaf(w2.y, qi[e], ak[e]);
+        av[e] = __builtin_fmaf(w2.x, gx[e], av[e]);
+      }
+      float kx[VEC], cj[HV], sj[HV];
+      widen<T>(load_split(k, j), kx);
+      pb.cs(j, cj, sj);
+      const float rkj = PL::rms_factor(kx, ProBase<T, LPR>::D, pb.eps);
+      PL::backward_w(ak, kx, rkj, pb.wk, cj, sj, ProBase<T, LPR>::D, dwk);
+      store_split<T>(dk, j, ak);
+      store_split<T>(dv, j, av);
+    }
+  }
+  write_wave_partial<T, LPR, true>(dwk, p.dwk_part, part0 + wave, p.D);
+}
+
 }  // namespace
 
 template <typename T, int LPR, int NM, bool FAR>
@@ -711,6 +1116,25 @@ hipError_t pro_pattern(bool fwd, const Params& p, const WalkCfg& c, int dtype, h
     hipLaunchKernelGGL((bwd_fused_pro<T, LPR, NM>), grid, block, kPipeLds, st, p, c);
     return hipGetLastError();
   } else {
+    if (c.column) {
+      const ChainCfg cc = make_chain_cfg(p.B, p.q.st * (int64_t)sizeof(T), c);
+      if (cc.nwg <= 0) return hipErrorInvalidValue;
+      const dim3 cgrid((unsigned)cc.nwg), cblock(64 * cc.W);
+      switch (cc.W) {
+        case 8: hipLaunchKernelGGL((bwd_chain_pro<T, LPR, NM, 8>), cgrid, cblock, 0, st, p, cc); break;
+        case 4: hipLaunchKernelGGL((bwd_chain_pro<T, LPR, NM, 4>), cgrid, cblock, 0, st, p, cc); break;
+        case 2: hipLaunchKernelGGL((bwd_chain_pro<T, LPR, NM, 2>), cgrid, cblock, 0, st, p, cc); break;
+        default: hipLaunchKernelGGL((bwd_chain_pro<T, LPR, NM, 1>), cgrid, cblock, 0, st, p, cc); break;
+      }
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      const int64_t fw = chain_pro_fix_waves(p.B, cc);
+      const int64_t fwg = (fw + 3) / 4;
+      if (fwg > 0x7fffffff) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((bwd_fix_pro<T, LPR>), dim3((unsigned)fwg), dim3(256), 0, st, p, cc,
+                         (int64_t)cc.nwg * cc.W);
+      return hipGetLastError();
+    }
     hipLaunchKernelGGL((bwd_q_pro<T, LPR, NM, FAR>), grid, block, kPipeLds, st, p, c);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

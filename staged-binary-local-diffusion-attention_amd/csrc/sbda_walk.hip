@@ -177,13 +177,24 @@ void walk_partials(const Params& p, int dtype, int64_t* pq, int64_t* pk, int64_t
     return;
   }
   if (c.column) {   // chained backward + finishing kernel (sbda_walk_pro.hip)
+    // The chain height depends on the row stride, which the size query does
+    // not see: with strides (a launch) the sizes of that chain height, without
+    // (a query, p.q.st == 0) the larger of the two heights' sizes.
     const int lpr = walk_lpr(p, dtype);
     const int esz = dtype == kFP32 ? 4 : 2;
-    const walk::ChainCfg cc = walk::make_chain_cfg(p.B, p.q.st * (int64_t)esz, c);
-    const int64_t slots = walk::chain_pro_slots(p.B, cc);
-    *pq = (int64_t)cc.nwg * cc.W;
-    *pk = *pq + 4 * ((walk::chain_pro_fix_waves(p.B, cc) + 3) / 4);
-    *tab_floats = slots * (walk::chain_pro_slot_floats(lpr, p.D) + 2 * (64 / lpr));
+    *pq = *pk = *tab_floats = 0;
+    for (int k = 0; k < 2; ++k) {
+      const int64_t stride = p.q.st > 0 ? p.q.st * (int64_t)esz : (k ? walk::kBigStride : 0);
+      const walk::ChainCfg cc = walk::make_chain_cfg(p.B, stride, c);
+      const int64_t q_ = (int64_t)cc.nwg * cc.W;
+      const int64_t k_ = q_ + 4 * ((walk::chain_pro_fix_waves(p.B, cc) + 3) / 4);
+      const int64_t t_ = walk::chain_pro_slots(p.B, cc) *
+                         (walk::chain_pro_slot_floats(lpr, p.D) + 2 * (64 / lpr));
+      *pq = std::max(*pq, q_);
+      *pk = std::max(*pk, k_);
+      *tab_floats = std::max(*tab_floats, t_);
+      if (p.q.st > 0) break;
+    }
     return;
   }
   *pq = (int64_t)c.nwg * c.waves;

@@ -264,6 +264,70 @@ def test_prologue_across_head_dims(dtype, h, d, layer):
         assert (a - w).abs().max().item() / scale < (2e-2 if dtype != torch.float32 else 1e-4), name
 
 
+def _check_prologue_against_oracle(q, k, v, g, offs, dtype, *, width=None, what=""):
+    """fused_sbda_prologue (autograd) against the oracle's prologue + gather
+    attention.  ``width``: place q/k/v as the first H heads of a ``width``-head
+    buffer, so their position stride is ``width * D`` elements."""
+    theta = 10000.0
+    b, t, h, d = q.shape
+    gen = torch.Generator().manual_seed(31 + d + t)
+    wq = (1 + 0.1 * torch.randn(d, generator=gen))
+    wk = (1 + 0.1 * torch.randn(d, generator=gen))
+
+    def place(x):
+        if width is None:
+            return _dev(x)
+        buf = torch.zeros(b, t, width, d, dtype=x.dtype, device=DEV)
+        buf[:, :, :h] = x.to(DEV)
+        return buf[:, :, :h].permute(0, 2, 1, 3)
+
+    qd, kd, vd = (place(x).detach().requires_grad_() for x in (q, k, v))
+    wqd, wkd = wq.to(DEV).requires_grad_(), wk.to(DEV).requires_grad_()
+    out = sbda_amd.fused_sbda_prologue(qd, kd, vd, torch.tensor(offs, dtype=torch.int32, device=DEV),
+                                       wqd, wkd, theta=theta)
+    out.backward(_dev(g))
+    torch.cuda.synchronize()
+    rq, rk, rv = (x.float().requires_grad_() for x in (q, k, v))
+    rwq, rwk = wq.clone().requires_grad_(), wk.clone().requires_grad_()
+    qq, kk = ref.prologue(rq, rk, rwq, rwk, theta)
+    want = ref.gather_attention(qq.permute(0, 2, 1, 3), kk.permute(0, 2, 1, 3), rv.permute(0, 2, 1, 3), offs)
+    want.backward(g.float().permute(0, 2, 1, 3))
+    tol = dict(rtol=1e-4, atol=1e-5) if dtype == torch.float32 else LOW_TOL
+    pairs = [("out", out, want), ("dq", qd.grad, rq.grad.permute(0, 2, 1, 3)),
+             ("dk", kd.grad, rk.grad.permute(0, 2, 1, 3)), ("dv", vd.grad, rv.grad.permute(0, 2, 1, 3))]
+    for name, a, w in pairs:
+        torch.testing.assert_close(a.detach().float().cpu(), w.detach(), **tol,
+                                   msg=lambda m: f"prologue {what} {name}: {m}")
+    for name, a, w in (("dwq", wqd.grad, rwq.grad), ("dwk", wkd.grad, rwk.grad)):
+        a = a.float().cpu()
+        scale = w.abs().max().item() + 1e-6
+        assert (a - w).abs().max().item() / scale < (2e-2 if dtype != torch.float32 else 1e-4), \
+            f"{what} {name}"
+
+
+@pytest.mark.parametrize("b,t,h,d,dtype,offs", [
+    (1, 1000, 8, 64, torch.bfloat16, (0, 1, 2, 16)),     # 63 rows of 16, last one partial
+    (2, 2048, 16, 64, torch.bfloat16, (0, 1, 2, 512)),   # 4 rows: 4-wave chains, 2 head groups
+    (1, 700, 8, 64, torch.bfloat16, (0, 1, 2, 512)),     # 2 rows, the second partial
+    (1, 300, 8, 64, torch.bfloat16, (0, 1, 2, 512)),     # 1 row: far source never valid
+    (1, 3000, 8, 64, torch.float16, (0, 64)),            # self + far only
+    (1, 2500, 8, 32, torch.float32, (0, 1, 2, 32)),
+    (3, 1200, 8, 64, torch.bfloat16, (0, 1, 2, 64)),     # 19 rows: chains of 8, 8 and 3
+])
+def test_chained_prologue_backward_edges(b, t, h, d, dtype, offs):
+    q, k, v, g = _inputs(b, t, h, d, dtype, seed=1300 + t + offs[-1])
+    _check_prologue_against_oracle(q, k, v, g, offs, dtype, what=f"b={b} t={t} offs={offs}")
+
+
+def test_chained_prologue_backward_wide_row_stride():
+    # q/k/v are 8 of 64 heads of their buffers: an 8 KiB position stride, so
+    # rows F = 4096 positions apart are 32 MiB apart and chains hold 4 rows.
+    b, t, h, d = 1, 8 * 4096, 8, 64
+    q, k, v, g = _inputs(b, t, h, d, torch.bfloat16, seed=1400)
+    _check_prologue_against_oracle(q, k, v, g, (0, 1, 2, 4096), torch.bfloat16, width=64,
+                                   what="wide stride")
+
+
 # --------------------------------------------------- metric-size properties
 
 @pytest.mark.parametrize("layer", [3, 20])

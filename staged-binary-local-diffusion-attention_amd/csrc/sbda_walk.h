@@ -196,6 +196,43 @@ __device__ inline void write_wave_partial(float (&x)[VecOf<T>::value], float* pa
   }
 }
 
+// Walk rows cover the head dimension exactly (LPR lanes x VEC elements = D),
+// so the per-wave rows below are complete.  Sums NV per-lane partials (x[0],
+// then x[1]) over the wave's heads, then over the workgroup's waves in wave
+// order through LDS `red` (NV * waves * D floats, free for reuse), and writes
+// row `row` of part[v] -- one row per workgroup instead of one per wave.
+// Deterministic; every thread of the workgroup must call it (one barrier,
+// plus one before `red` is written when it held other data).
+template <typename T, int LPR, int NV>
+__device__ inline void write_group_partials(float (&x)[NV][VecOf<T>::value], float* red, int waves,
+                                            float* const (&part)[NV], int64_t row, int D) {
+  constexpr int VEC = VecOf<T>::value;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+#pragma unroll
+      for (int m = LPR; m < 64; m <<= 1) x[v][e] += __shfl_xor(x[v][e], m, 64);
+    }
+  }
+  __syncthreads();
+  if (lane < LPR) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) red[(v * waves + w) * D + elem_index<T, true>(lane, e, D)] = x[v][e];
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < NV * D; i += 64 * waves) {
+    const int v = i / D, d = i % D;
+    float s = 0.f;
+    for (int k = 0; k < waves; ++k) s += red[(v * waves + k) * D + d];
+    part[v][row * D + d] = s;
+  }
+}
+
 // ========================================================= pipelined walks
 //
 // Software-pipelined walks (no prologue): while step u is computed, every

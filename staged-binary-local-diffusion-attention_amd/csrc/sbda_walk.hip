@@ -186,8 +186,9 @@ void walk_partials(const Params& p, int dtype, int64_t* pq, int64_t* pk, int64_t
     for (int k = 0; k < 2; ++k) {
       const int64_t stride = p.q.st > 0 ? p.q.st * (int64_t)esz : (k ? walk::kBigStride : 0);
       const walk::ChainCfg cc = walk::make_chain_cfg(p.B, stride, c);
-      const int64_t q_ = (int64_t)cc.nwg * cc.W;
-      const int64_t k_ = q_ + 4 * ((walk::chain_pro_fix_waves(p.B, cc) + 3) / 4);
+      // One partial row per workgroup of either kernel.
+      const int64_t q_ = cc.nwg;
+      const int64_t k_ = q_ + (walk::chain_pro_fix_waves(p.B, cc) + 3) / 4;
       const int64_t t_ = walk::chain_pro_slots(p.B, cc) *
                          (walk::chain_pro_slot_floats(lpr, p.D) + 2 * (64 / lpr));
       *pq = std::max(*pq, q_);

@@ -962,7 +962,7 @@ struct BwdChainPro : ProBase<T, LPR> {
 template <typename T, int LPR, int NM, bool LEFT_LDS, bool RIGHT_LDS, int W>
 __device__ inline void chain_pro_wave(const Params& p, const ChainCfg& c,
                                       ChainProSlot<VecOf<T>::value>* lds, int w, int b, int hg,
-                                      int rb, int cb, int a, int64_t wave) {
+                                      int rb, int cb, int a, float (&dw)[2][VecOf<T>::value]) {
   constexpr int VEC = VecOf<T>::value, esz = (int)sizeof(T);
   const int lane = threadIdx.x & 63, hl = lane / LPR, li = lane % LPR;
   const int h0 = hg * (64 / LPR);
@@ -998,8 +998,11 @@ __device__ inline void chain_pro_wave(const Params& p, const ChainCfg& c,
   float2* pcs = reinterpret_cast<float2*>(p.tab + slots * chain_pro_slot_floats(LPR, p.D));
   x.defer_pc = (!LEFT_LDS && rb > 0) ? pcs + (slot0 - c.F) * (64 / LPR) : nullptr;
   x.walk(a - 2, a + c.P + 1);
-  write_wave_partial<T, LPR, true>(x.dwq, p.dwq_part, wave, p.D);
-  write_wave_partial<T, LPR, true>(x.dwk, p.dwk_part, wave, p.D);
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    dw[0][e] = x.dwq[e];
+    dw[1][e] = x.dwk[e];
+  }
 }
 
 template <typename T, int LPR, int NM, int W>
@@ -1018,31 +1021,37 @@ __global__ __launch_bounds__(64 * W) void bwd_chain_pro(Params p, ChainCfg c) {
   const int r = rb * W + w;
   const int64_t a64 = (int64_t)r * c.F + (int64_t)cb * c.P;
   const int a = (r < c.rows && a64 < p.T) ? (int)a64 : p.T;
-  const int64_t wave = (int64_t)blockIdx.x * W + w;
+  float dw[2][VecOf<T>::value];
   if constexpr (W == 1) {
-    chain_pro_wave<T, LPR, NM, false, false, W>(p, c, lds, w, b, hg, rb, cb, a, wave);
+    chain_pro_wave<T, LPR, NM, false, false, W>(p, c, lds, w, b, hg, rb, cb, a, dw);
   } else {
     if (w == 0)
-      chain_pro_wave<T, LPR, NM, false, true, W>(p, c, lds, w, b, hg, rb, cb, a, wave);
+      chain_pro_wave<T, LPR, NM, false, true, W>(p, c, lds, w, b, hg, rb, cb, a, dw);
     else if (w == W - 1)
-      chain_pro_wave<T, LPR, NM, true, false, W>(p, c, lds, w, b, hg, rb, cb, a, wave);
+      chain_pro_wave<T, LPR, NM, true, false, W>(p, c, lds, w, b, hg, rb, cb, a, dw);
     else
-      chain_pro_wave<T, LPR, NM, true, true, W>(p, c, lds, w, b, hg, rb, cb, a, wave);
+      chain_pro_wave<T, LPR, NM, true, true, W>(p, c, lds, w, b, hg, rb, cb, a, dw);
   }
+  // One norm-weight partial row per workgroup (the rings' LDS is free now).
+  float* const parts[2] = {p.dwq_part, p.dwk_part};
+  write_group_partials<T, LPR, 2>(dw, reinterpret_cast<float*>(lds), W, parts, blockIdx.x, p.D);
 }
 
 // Finishes the deferred keys: the last row of every chain (row rb * W + W - 1)
-// whose far query j + F exists.  One wave per kFixCols columns of a row, no
-// barriers.  dK' = near part + c * roped q_{j+F}, dV = near part + p * dO_{j+F},
-// then the transposed prologue as in the chained walk.
+// whose far query j + F exists.  One wave per kFixCols columns of a row (the
+// loop has no barriers; the workgroup's partial row at the end has two).
+// dK' = near part + c * roped q_{j+F}, dV = near part + p * dO_{j+F}, then the
+// transposed prologue as in the chained walk.
 template <typename T, int LPR>
 __global__ __launch_bounds__(256) void bwd_fix_pro(Params p, ChainCfg c, int64_t part0) {
   constexpr int VEC = VecOf<T>::value, HV = VEC / 2, esz = (int)sizeof(T);
   using PL = Prologue<T, LPR>;
+  __shared__ float red[4 * 128];
   const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int chunks = (c.F + kFixCols - 1) / kFixCols;
   const int64_t nwaves = chain_pro_fix_waves(p.B, c);
-  float dwk[VEC];
+  float dw[1][VEC];
+  float (&dwk)[VEC] = dw[0];
 #pragma unroll
   for (int e = 0; e < VEC; ++e) dwk[e] = 0.f;
   if (wave < nwaves) {
@@ -1100,7 +1109,8 @@ __global__ __launch_bounds__(256) void bwd_fix_pro(Params p, ChainCfg c, int64_t
       store_split<T>(dv, j, av);
     }
   }
-  write_wave_partial<T, LPR, true>(dwk, p.dwk_part, part0 + wave, p.D);
+  float* const parts[1] = {p.dwk_part};
+  write_group_partials<T, LPR, 1>(dw, red, 4, parts, part0 + blockIdx.x, p.D);
 }
 
 }  // namespace
@@ -1132,7 +1142,7 @@ hipError_t pro_pattern(bool fwd, const Params& p, const WalkCfg& c, int dtype, h
       const int64_t fwg = (fw + 3) / 4;
       if (fwg > 0x7fffffff) return hipErrorInvalidValue;
       hipLaunchKernelGGL((bwd_fix_pro<T, LPR>), dim3((unsigned)fwg), dim3(256), 0, st, p, cc,
-                         (int64_t)cc.nwg * cc.W);
+                         (int64_t)cc.nwg);
       return hipGetLastError();
     }
     hipLaunchKernelGGL((bwd_q_pro<T, LPR, NM, FAR>), grid, block, kPipeLds, st, p, c);

@@ -111,19 +111,27 @@ inline ChainCfg make_chain_cfg(int64_t B, int64_t row_stride_bytes, const WalkCf
 
 // Chained prologue backward (far F >= 16): the keys of a chain's last row
 // whose far query lies in the next chain are finished by a second kernel
-// from a workspace of deferred slots, one per (batch, head group, row block,
-// column): the key's near-slot dK' and dV rows (fp32, 64 / LPR heads x D
-// each) and the far query's weight pair per head.
+// from a workspace of deferred slots, one per (batch, head group, row block
+// but the last, column): the key's near-slot dK' and dV rows (fp32, 64 / LPR
+// heads x D each) and the far query's weight pair per head.  The last row
+// block has no next chain, so nothing of it is deferred.
 constexpr int kFixCols = 8;   // deferred columns per finishing wave
 
+__host__ __device__ inline int64_t chain_pro_deferring_blocks(const ChainCfg& c) {
+  return c.blocks > 1 ? c.blocks - 1 : 0;
+}
 __host__ __device__ inline int64_t chain_pro_slots(int64_t B, const ChainCfg& c) {
-  return B * c.HG * c.blocks * c.F;
+  return B * c.HG * chain_pro_deferring_blocks(c) * c.F;
+}
+// Slot of (batch, head group, row block rb < blocks - 1, column).
+__host__ __device__ inline int64_t chain_pro_slot(const ChainCfg& c, int b, int hg, int rb, int col) {
+  return (((int64_t)b * c.HG + hg) * chain_pro_deferring_blocks(c) + rb) * c.F + col;
 }
 __host__ __device__ inline int64_t chain_pro_slot_floats(int lpr, int D) {
   return 2 * (64 / lpr) * (int64_t)D;
 }
 __host__ __device__ inline int64_t chain_pro_fix_waves(int64_t B, const ChainCfg& c) {
-  return B * c.HG * c.blocks * ((c.F + kFixCols - 1) / kFixCols);
+  return B * c.HG * chain_pro_deferring_blocks(c) * ((c.F + kFixCols - 1) / kFixCols);
 }
 
 // Workgroups are dealt to the 8 XCDs round-robin; give each XCD a contiguous

@@ -927,7 +927,7 @@ struct BwdChainPro : ProBase<T, LPR> {
         }
         finish_key<R>(j, ak, av);
       } else {
-        if (there) {
+        if (there && defer != nullptr) {
           // Far query in the next chain: bwd_fix_pro finishes this key.
           float4* slot = defer + (int64_t)(j - a) * (2 * (VEC / 4) * 64);
 #pragma unroll
@@ -991,12 +991,17 @@ __device__ inline void chain_pro_wave(const Params& p, const ChainCfg& c,
   x.mine = lds + w;
   x.up = lds + (LEFT_LDS ? w - 1 : w);
   x.down = lds + (RIGHT_LDS ? w + 1 : w);
-  // Deferred slots: index ((b * HG + hg) * blocks + row block) * F + column.
+  // Deferred slots (row blocks but the last): this wave's band in block rb
+  // (last wave) and in block rb - 1 (first wave, far weight pairs).
   const int64_t slots = chain_pro_slots(p.B, c);
-  const int64_t slot0 = (((int64_t)b * c.HG + hg) * c.blocks + rb) * c.F + (int64_t)cb * c.P;
-  x.defer = reinterpret_cast<float4*>(p.tab) + slot0 * (2 * (VEC / 4) * 64);
+  const int last_block = c.blocks - 1;
+  x.defer = rb < last_block
+                ? reinterpret_cast<float4*>(p.tab) +
+                      chain_pro_slot(c, b, hg, rb, cb * c.P) * (2 * (VEC / 4) * 64)
+                : nullptr;   // the last block's keys have no far query
   float2* pcs = reinterpret_cast<float2*>(p.tab + slots * chain_pro_slot_floats(LPR, p.D));
-  x.defer_pc = (!LEFT_LDS && rb > 0) ? pcs + (slot0 - c.F) * (64 / LPR) : nullptr;
+  x.defer_pc = (!LEFT_LDS && rb > 0) ? pcs + chain_pro_slot(c, b, hg, rb - 1, cb * c.P) * (64 / LPR)
+                                     : nullptr;
   x.walk(a - 2, a + c.P + 1);
 #pragma unroll
   for (int e = 0; e < VEC; ++e) {
@@ -1058,8 +1063,9 @@ __global__ __launch_bounds__(256) void bwd_fix_pro(Params p, ChainCfg c, int64_t
     int64_t g = wave;
     const int chunk = (int)(g % chunks);
     g /= chunks;
-    const int rb = (int)(g % c.blocks);
-    g /= c.blocks;
+    const int nb = (int)chain_pro_deferring_blocks(c);
+    const int rb = (int)(g % nb);
+    g /= nb;
     const int hg = (int)(g % c.HG);
     const int b = (int)(g / c.HG);
     const int r = rb * c.W + c.W - 1;
@@ -1080,7 +1086,7 @@ __global__ __launch_bounds__(256) void bwd_fix_pro(Params p, ChainCfg c, int64_t
       const int64_t j64 = (int64_t)r * c.F + col;
       if (c.W < 2 || r >= c.rows || j64 + c.F >= p.T) continue;
       const int j = (int)j64, i = j + c.F;
-      const int64_t slot = (((int64_t)b * c.HG + hg) * c.blocks + rb) * c.F + col;
+      const int64_t slot = chain_pro_slot(c, b, hg, rb, col);
       const float4* sr = rows + slot * (2 * (VEC / 4) * 64);
       float ak[VEC], av[VEC];
 #pragma unroll
@@ -1141,6 +1147,7 @@ hipError_t pro_pattern(bool fwd, const Params& p, const WalkCfg& c, int dtype, h
       const int64_t fw = chain_pro_fix_waves(p.B, cc);
       const int64_t fwg = (fw + 3) / 4;
       if (fwg > 0x7fffffff) return hipErrorInvalidValue;
+      if (fwg == 0) return hipSuccess;   // a single row block defers nothing
       hipLaunchKernelGGL((bwd_fix_pro<T, LPR>), dim3((unsigned)fwg), dim3(256), 0, st, p, cc,
                          (int64_t)cc.nwg);
       return hipGetLastError();

@@ -17,12 +17,10 @@ Device tensors only; errors follow the attention ops' classes.
 
 from __future__ import annotations
 
-import ctypes
-
 import torch
 
 from . import _lib
-from .sbda import _DTYPES, _ptr
+from .sbda import _DTYPES, _on_device, _ptr, _stream
 
 
 def _rows(x: torch.Tensor, width: int) -> torch.Tensor:
@@ -36,10 +34,6 @@ def _rows(x: torch.Tensor, width: int) -> torch.Tensor:
     if x.data_ptr() % 16:
         x = x.clone()
     return x
-
-
-def _stream(x: torch.Tensor) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
 
 
 class _AddRMSNorm(torch.autograd.Function):
@@ -56,7 +50,7 @@ class _AddRMSNorm(torch.autograd.Function):
         s = torch.empty_like(xs) if rs is not None else xs
         rstd = torch.empty(rows, dtype=torch.float32, device=x.device)
         lib = _lib.load()
-        with torch.cuda.device(x.device):
+        with _on_device(x.device):
             _lib.check(lib.sbda_rmsnorm_forward(
                 _ptr(xs), _ptr(rs), _ptr(s if rs is not None else None), _ptr(y), _ptr(w32),
                 _ptr(rstd), rows, dim, _DTYPES[x.dtype], float(eps), _stream(x)))
@@ -85,7 +79,7 @@ class _AddRMSNorm(torch.autograd.Function):
         if need < 0:
             _lib.check(-need)
         ws = torch.empty(max(int(need), 16), dtype=torch.uint8, device=s.device)
-        with torch.cuda.device(s.device):
+        with _on_device(s.device):
             _lib.check(lib.sbda_rmsnorm_backward(
                 _ptr(dy), _ptr(s), _ptr(w32), _ptr(rstd), _ptr(ds), _ptr(dx), _ptr(dw), _ptr(ws),
                 ws.numel(), rows, dim, _DTYPES[s.dtype], _stream(s)))
@@ -117,7 +111,7 @@ class _SwiGLU(torch.autograd.Function):
         rows = gu.numel() // two_h
         out = torch.empty(*gu.shape[:-1], hidden, dtype=gu.dtype, device=gu.device)
         lib = _lib.load()
-        with torch.cuda.device(gu.device):
+        with _on_device(gu.device):
             _lib.check(lib.sbda_swiglu_forward(_ptr(gu), _ptr(out), rows, hidden,
                                                _DTYPES[gu.dtype], _stream(gu)))
         ctx.save_for_backward(gu)
@@ -132,7 +126,7 @@ class _SwiGLU(torch.autograd.Function):
         d = _rows(dout.to(gu.dtype), hidden)
         dgu = torch.empty_like(gu)
         lib = _lib.load()
-        with torch.cuda.device(gu.device):
+        with _on_device(gu.device):
             _lib.check(lib.sbda_swiglu_backward(_ptr(d), _ptr(gu), _ptr(dgu), rows, hidden,
                                                 _DTYPES[gu.dtype], _stream(gu)))
         return dgu

@@ -33,6 +33,7 @@ implementation.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import weakref
 from collections import OrderedDict
@@ -80,13 +81,34 @@ def _dense_like(t: torch.Tensor) -> torch.Tensor:
     ``t``'s stride order -- ``empty_like`` for dense tensors, and for a
     strided view (q sliced out of a fused QKV projection) the same
     position-major order instead of PyTorch's contiguous fallback."""
+    if t.ndim == 4 and t.transpose(1, 2).is_contiguous():
+        return torch.empty_like(t)   # [B,T,H,D] memory seen as [B,H,T,D]: strides kept
     order = sorted(range(t.ndim), key=lambda i: -t.stride(i))
     base = torch.empty([t.shape[i] for i in order], dtype=t.dtype, device=t.device)
     return base.permute([order.index(i) for i in range(t.ndim)])
 
 
+if hasattr(torch._C, "_cuda_getCurrentRawStream"):
+    _raw_stream = torch._C._cuda_getCurrentRawStream
+else:                                         # pragma: no cover - other torch builds
+    def _raw_stream(index: int) -> int:
+        return torch.cuda.current_stream(index).cuda_stream
+
+
 def _stream(t: torch.Tensor) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    """The current stream of ``t``'s device (the one torch's own kernels use)."""
+    index = t.device.index
+    return ctypes.c_void_p(_raw_stream(torch.cuda.current_device() if index is None else index))
+
+
+_NO_GUARD = contextlib.nullcontext()
+
+
+def _on_device(device: torch.device):
+    """A device guard that switches only when ``device`` is not current."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        return _NO_GUARD
+    return torch.cuda.device(device)
 
 
 def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
@@ -168,7 +190,7 @@ def _lse_storage(b: int, h: int, t: int, device) -> torch.Tensor:
     """Per-row log-normalisers, stored position-major ``[B, T, H]`` (each
     position's heads are adjacent, as in q/k/v memory) and handed out as a
     ``[B, H, T]`` view."""
-    return torch.empty((b, t, h), dtype=torch.float32, device=device).permute(0, 2, 1)
+    return torch.empty_strided((b, h, t), (t * h, 1, h), dtype=torch.float32, device=device)
 
 
 def _lse_buffer(lse: torch.Tensor) -> torch.Tensor:
@@ -186,7 +208,7 @@ def sbda_forward(q, k, v, offsets, seg_key=None) -> tuple[torch.Tensor, torch.Te
     out = _dense_like(q)
     b, h, t, _ = q.shape
     lse = _lse_storage(b, h, t, q.device)
-    with torch.cuda.device(q.device):
+    with _on_device(q.device):
         _lib.check(lib.sbda_forward(
             _ptr(q), _lib.strides(q), _ptr(k), _lib.strides(k), _ptr(v), _lib.strides(v),
             _ptr(out), _lib.strides(out), _ptr(lse), *_shape_args(q, k, offs),
@@ -212,7 +234,7 @@ def sbda_backward(q, k, v, grad_out, lse, offsets, seg_key=None):
     if need < 0:
         _lib.check(-need)
     ws = torch.empty(int(need), dtype=torch.uint8, device=q.device) if need else None
-    with torch.cuda.device(q.device):
+    with _on_device(q.device):
         _lib.check(lib.sbda_backward(
             _ptr(q), _lib.strides(q), _ptr(k), _lib.strides(k), _ptr(v), _lib.strides(v),
             _ptr(grad_out), _lib.strides(grad_out), _ptr(lse),
@@ -304,7 +326,7 @@ def sbda_forward_paths(q, k, v, path_indices, path_valid=None, seg_key=None, *, 
     out = _dense_like(q)
     b, h, t, _ = q.shape
     lse = _lse_storage(b, h, t, q.device)
-    with torch.cuda.device(q.device):
+    with _on_device(q.device):
         _lib.check(lib.sbda_forward_paths(
             _ptr(q), _lib.strides(q), _ptr(k), _lib.strides(k), _ptr(v), _lib.strides(v),
             _ptr(out), _lib.strides(out), _ptr(lse), *_prologue_ptrs(prologue),
@@ -338,7 +360,7 @@ def sbda_backward_paths(q, k, v, grad_out, lse, path_indices, path_valid=None, s
         _lib.check(-need)
     ws = torch.empty(int(need) + 256, dtype=torch.uint8, device=q.device)
     ws_view = ws[(-ws.data_ptr()) % 256:]
-    with torch.cuda.device(q.device):
+    with _on_device(q.device):
         _lib.check(lib.sbda_backward_paths(
             _ptr(q), _lib.strides(q), _ptr(k), _lib.strides(k), _ptr(v), _lib.strides(v),
             _ptr(grad_out), _lib.strides(grad_out), _ptr(lse), *_prologue_ptrs(prologue),
@@ -442,7 +464,7 @@ class _FusedSBDAPrologue(torch.autograd.Function):
         cos, sin = rope_tables(t, d, theta, q.device)
         out = _dense_like(q)
         lse = _lse_storage(b, h, t, q.device)
-        with torch.cuda.device(q.device):
+        with _on_device(q.device):
             _lib.check(lib.sbda_forward_prologue(
                 _ptr(q), _lib.strides(q), _ptr(k), _lib.strides(k), _ptr(v), _lib.strides(v),
                 _ptr(out), _lib.strides(out), _ptr(lse), _ptr(wq), _ptr(wk), _ptr(cos), _ptr(sin),
@@ -470,7 +492,7 @@ class _FusedSBDAPrologue(torch.autograd.Function):
         if need < 0:
             _lib.check(-need)
         ws = torch.empty(max(int(need), 16), dtype=torch.uint8, device=q.device)
-        with torch.cuda.device(q.device):
+        with _on_device(q.device):
             _lib.check(lib.sbda_backward_prologue(
                 _ptr(q), _lib.strides(q), _ptr(k), _lib.strides(k), _ptr(v), _lib.strides(v),
                 _ptr(g), _lib.strides(g), _ptr(lse), _ptr(wq), _ptr(wk), _ptr(cos), _ptr(sin),

@@ -425,6 +425,16 @@ def test_walk_kernels_across_head_groups_and_row_widths(dtype, tol, b, h, d, off
            f"{dtype} B={b} H={h} D={d} {offs}")
 
 
+@pytest.mark.parametrize("t,offs", [(16384, (0, 1, 2, 4096)), (32768, (0, 1, 2, 8192)),
+                                    (20000, (0, 1, 2, 4096))])
+def test_walk_forward_row_groups_at_4_to_8_mib_strides(t, offs):
+    # Far rows 4-8 MiB apart (1 KiB positions): the forward walks 8 rows x 1
+    # band per workgroup there instead of 2 rows x 4 bands; T = 20000 leaves
+    # a partial last row.
+    q, k, v, g = _inputs(1, t, 8, 64, torch.bfloat16, seed=t + offs[-1])
+    _close(_fused(q, k, v, offs, g), _oracle(q, k, v, offs, g), LOW_TOL, f"T={t} {offs}")
+
+
 # ------------------------------------------------------------ module level
 
 def _oracle_module_forward(m, x, valid_mask=None, seam_reset=None, path_indices=None,

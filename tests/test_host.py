@@ -107,6 +107,25 @@ def test_host_offsets_cache():
     assert sbda_amd.host_offsets([0, 2]) == (0, 2)
 
 
+def test_outputs_keep_the_inputs_position_major_layout():
+    # Outputs and gradients are allocated dense in the input's stride order:
+    # [B,T,H,D] memory seen as [B,H,T,D] (the reference's empty_like(q)), a
+    # q sliced out of a fused [B,T,3,H,D] projection, and a plain [B,H,T,D].
+    S = sbda_amd.sbda
+    x = torch.randn(2, 5, 3, 4)                                  # [B,T,H,D]
+    views = [x.permute(0, 2, 1, 3),
+             torch.randn(2, 5, 3, 3, 4)[:, :, 0].permute(0, 2, 1, 3),
+             torch.randn(2, 3, 5, 4)]
+    for v in views:
+        out = S._dense_like(v)
+        assert out.shape == v.shape
+        order = sorted(range(4), key=lambda i: -v.stride(i))
+        assert sorted(range(4), key=lambda i: -out.stride(i)) == order
+        assert out.is_contiguous() or out.permute(order).is_contiguous()
+    lse = S._lse_storage(2, 3, 5, "cpu")
+    assert lse.shape == (2, 3, 5) and lse.permute(0, 2, 1).is_contiguous()
+
+
 def test_topology_matches_oracle_and_reference_statistics():
     for layer in range(1, 24):
         assert sbda_amd.topology_offsets(layer, topology="sbda") == ref.sbda_layer_offsets(layer)

@@ -139,7 +139,9 @@ int sbda_forward_prologue(const void* q_raw, const int64_t* q_strides,
                           const int32_t* offsets, int32_t num_offsets,
                           const int32_t* seg_key, void* stream);
 
-/* Workspace bytes sbda_backward_prologue needs for these shapes (< 0: error). */
+/* Workspace bytes sbda_backward_prologue needs for these shapes (< 0: error);
+ * enough for any strides of the tensors (the launch uses what its strides
+ * need, at most this). */
 int64_t sbda_backward_prologue_workspace(int64_t batch, int64_t heads, int64_t kv_heads,
                                          int64_t length, int64_t head_dim, int32_t dtype,
                                          const int32_t* offsets, int32_t num_offsets,

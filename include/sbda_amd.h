@@ -93,8 +93,11 @@ int sbda_forward(const void* q, const int64_t* q_strides,
                  const int32_t* offsets, int32_t num_offsets,
                  const int32_t* seg_key, void* stream);
 
-/* Workspace bytes sbda_backward needs for these shapes and masks (0 for the
- * wavefront-walk kernels; < 0: error). */
+/* Workspace bytes sbda_backward needs for these shapes and masks (< 0:
+ * error), enough for any strides: when the strides could send the call to the
+ * generic kernels (row spans past 4 GiB) it is their weight table, although
+ * the wavefront-walk kernels need none.  sbda_backward_workspace_for gives the
+ * exact figure for given strides (0 on the walk path). */
 int64_t sbda_backward_workspace(int64_t batch, int64_t heads, int64_t kv_heads,
                                 int64_t length, int64_t head_dim, int32_t dtype,
                                 const int32_t* offsets, int32_t num_offsets,
@@ -140,12 +143,29 @@ int sbda_forward_prologue(const void* q_raw, const int64_t* q_strides,
                           const int32_t* seg_key, void* stream);
 
 /* Workspace bytes sbda_backward_prologue needs for these shapes (< 0: error);
- * enough for any strides of the tensors (the launch uses what its strides
- * need, at most this). */
+ * enough for any strides of the tensors (sbda_backward_workspace_for: the
+ * exact figure for given strides). */
 int64_t sbda_backward_prologue_workspace(int64_t batch, int64_t heads, int64_t kv_heads,
                                          int64_t length, int64_t head_dim, int32_t dtype,
                                          const int32_t* offsets, int32_t num_offsets,
                                          const int32_t* seg_key);
+
+/*
+ * Workspace bytes sbda_backward (prologue = 0) or sbda_backward_prologue
+ * (prologue != 0) needs for these shapes and these strides of q, k, v,
+ * grad_out, dq, dk, dv (< 0: error).  Exact: the strides decide between the
+ * kernel families (row spans past 4 GiB go to the generic kernels), which the
+ * stride-less queries above can only bound.  No counterpart in the reference
+ * (its Triton launches allocate their own tables).
+ */
+int64_t sbda_backward_workspace_for(int32_t prologue, const int64_t* q_strides,
+                                    const int64_t* k_strides, const int64_t* v_strides,
+                                    const int64_t* dout_strides, const int64_t* dq_strides,
+                                    const int64_t* dk_strides, const int64_t* dv_strides,
+                                    int64_t batch, int64_t heads, int64_t kv_heads,
+                                    int64_t length, int64_t head_dim, int32_t dtype,
+                                    const int32_t* offsets, int32_t num_offsets,
+                                    const int32_t* seg_key);
 
 /*
  * Backward of sbda_forward_prologue: gradients of the raw q/k, of v and of

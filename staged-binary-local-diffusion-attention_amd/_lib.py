@@ -11,7 +11,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("libsbda_amd.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 OK, ERR_VALUE, ERR_DTYPE, ERR_RUNTIME = 0, 1, 2, 3
 _ERRORS = {ERR_VALUE: ValueError, ERR_DTYPE: TypeError, ERR_RUNTIME: RuntimeError}
@@ -41,6 +41,7 @@ SIGNATURES = {
                                              _strides, _fptr, _fptr, _fptr, _p, _p, _f32,
                                              *_SHAPE, _SEG, _p]),
     "sbda_backward_prologue_workspace": (ctypes.c_int64, [*_SHAPE, _SEG]),
+    "sbda_backward_workspace_for": (ctypes.c_int64, [_i32, *[_strides] * 7, *_SHAPE, _SEG]),
     "sbda_backward_prologue": (ctypes.c_int, [_p, _strides, _p, _strides, _p, _strides, _p,
                                               _strides, _fptr, _fptr, _fptr, _p, _p, _f32,
                                               _p, _strides, _p, _strides, _p, _strides,

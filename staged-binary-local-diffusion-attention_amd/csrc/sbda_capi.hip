@@ -191,14 +191,24 @@ int forward_impl(bool pro, const void* q, const int64_t* qs, const void* k, cons
 int64_t workspace_floats(const Params& p, int dtype, bool pro, int64_t* pq, int64_t* pk) {
   int64_t tab = 0;
   *pq = *pk = 0;
-  if (walk_applies(p, dtype)) {
-    if (!pro) return 0;
-    walk_partials(p, dtype, pq, pk, &tab);
+  const bool walk = walk_applies(p, dtype);
+  if (walk) {
+    if (pro) walk_partials(p, dtype, pq, pk, &tab);
   } else {
     direct_partials(p, esize(dtype), pq, pk, &tab);
     if (!pro) *pq = *pk = 0;
   }
-  return (*pq + *pk) * p.D + tab;
+  const int64_t need = (*pq + *pk) * p.D + tab;
+  if (walk && p.q.p == nullptr) {
+    // A size query (no tensors, so no strides): strides can still send the
+    // launch to the generic kernels (a row span past 4 GiB), so report the
+    // larger of the two needs.  A launch lays out exactly its own need.
+    int64_t dq = 0, dk = 0, dtab = 0;
+    direct_partials(p, esize(dtype), &dq, &dk, &dtab);
+    if (!pro) dq = dk = 0;
+    return std::max(need, (dq + dk) * p.D + dtab);
+  }
+  return need;
 }
 
 int backward_impl(bool pro, const void* q, const int64_t* qs, const void* k, const int64_t* ks,
@@ -360,7 +370,7 @@ using namespace sbda;
 
 extern "C" {
 
-int sbda_abi_version(void) { return 7; }
+int sbda_abi_version(void) { return 8; }
 
 const char* sbda_last_error(void) { return g_error.c_str(); }
 
@@ -383,6 +393,34 @@ int64_t sbda_backward_workspace(int64_t batch, int64_t heads, int64_t kv_heads, 
   p.seg = seg_key;
   int64_t pq = 0, pk = 0;
   return workspace_floats(p, dtype, false, &pq, &pk) * (int64_t)sizeof(float);
+}
+
+int64_t sbda_backward_workspace_for(int32_t prologue, const int64_t* q_strides,
+                                    const int64_t* k_strides, const int64_t* v_strides,
+                                    const int64_t* dout_strides, const int64_t* dq_strides,
+                                    const int64_t* dk_strides, const int64_t* dv_strides,
+                                    int64_t batch, int64_t heads, int64_t kv_heads,
+                                    int64_t length, int64_t head_dim, int32_t dtype,
+                                    const int32_t* offsets, int32_t n, const int32_t* seg_key) {
+  g_error.clear();
+  Params p;
+  int rc = check_problem(batch, heads, kv_heads, length, head_dim, dtype, offsets, n, p);
+  if (rc) return -rc;
+  p.seg = seg_key;
+  // The strides decide between the kernel families; the tensors themselves
+  // are not needed (a 16-byte-aligned stand-in address passes the checks and
+  // is never dereferenced).
+  const void* stand_in = reinterpret_cast<const void*>(uintptr_t(16));
+  const int esz = esize(dtype);
+  if ((rc = check_view("q", stand_in, q_strides, esz, false, &p.q))) return -rc;
+  if ((rc = check_view("k", stand_in, k_strides, esz, false, &p.k))) return -rc;
+  if ((rc = check_view("v", stand_in, v_strides, esz, false, &p.v))) return -rc;
+  if ((rc = check_view("grad_out", stand_in, dout_strides, esz, false, &p.dout))) return -rc;
+  if ((rc = check_mut("dq", const_cast<void*>(stand_in), dq_strides, esz, &p.dq))) return -rc;
+  if ((rc = check_mut("dk", const_cast<void*>(stand_in), dk_strides, esz, &p.dk))) return -rc;
+  if ((rc = check_mut("dv", const_cast<void*>(stand_in), dv_strides, esz, &p.dv))) return -rc;
+  int64_t pq = 0, pk = 0;
+  return workspace_floats(p, dtype, prologue != 0, &pq, &pk) * (int64_t)sizeof(float);
 }
 
 int sbda_backward(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,

@@ -184,6 +184,16 @@ def _seg_arg(seg_key: torch.Tensor | None, q: torch.Tensor) -> ctypes.c_void_p:
     return ctypes.c_void_p(seg_key.data_ptr())
 
 
+def _workspace_bytes(lib, prologue: bool, views, shape, seg) -> int:
+    """Exact backward workspace for these tensors' strides (q, k, v, grad_out,
+    dq, dk, dv): the strides decide between the walk and generic kernels."""
+    need = lib.sbda_backward_workspace_for(int(prologue), *(_lib.strides(x) for x in views),
+                                           *shape, seg)
+    if need < 0:
+        _lib.check(-need)
+    return int(need)
+
+
 # -------------------------------------------------------- raw entry points
 
 def _lse_storage(b: int, h: int, t: int, device) -> torch.Tensor:
@@ -230,9 +240,7 @@ def sbda_backward(q, k, v, grad_out, lse, offsets, seg_key=None):
     dq, dk, dv = _dense_like(q), _dense_like(k), _dense_like(v)
     shape = _shape_args(q, k, offs)
     seg = _seg_arg(seg_key, q)
-    need = lib.sbda_backward_workspace(*shape, seg)
-    if need < 0:
-        _lib.check(-need)
+    need = _workspace_bytes(lib, False, (q, k, v, grad_out, dq, dk, dv), shape, seg)
     ws = torch.empty(int(need), dtype=torch.uint8, device=q.device) if need else None
     with _on_device(q.device):
         _lib.check(lib.sbda_backward(
@@ -488,9 +496,7 @@ class _FusedSBDAPrologue(torch.autograd.Function):
         dwk = torch.empty_like(dwq)
         shape = _shape_args(q, k, offs)
         seg = _seg_arg(ctx.seg_key, q)
-        need = lib.sbda_backward_prologue_workspace(*shape, seg)
-        if need < 0:
-            _lib.check(-need)
+        need = _workspace_bytes(lib, True, (q, k, v, g, dq, dk, dv), shape, seg)
         ws = torch.empty(max(int(need), 16), dtype=torch.uint8, device=q.device)
         with _on_device(q.device):
             _lib.check(lib.sbda_backward_prologue(

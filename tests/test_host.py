@@ -107,6 +107,35 @@ def test_host_offsets_cache():
     assert sbda_amd.host_offsets([0, 2]) == (0, 2)
 
 
+def test_backward_workspace_queries():
+    # Host-only calls.  Position-major [B,T,H,D] strides: the walk kernels
+    # need no workspace without the prologue; a row span past 4 GiB (64 heads
+    # x 64 x bf16 at T = 2^20) sends the call to the generic kernels, which
+    # need their weight table; the stride-less queries bound every case.
+    lib = _lib.load()
+    offs = _lib.offsets_array((0, 1, 2, 4096))
+
+    def strides(t, h, d):          # [1,T,H,D] memory seen as [1,H,T,D]
+        return (ctypes.c_int64 * 4)(t * h * d, d, h * d, 1)
+
+    def exact(pro, t, h, d):
+        s = strides(t, h, d)
+        return lib.sbda_backward_workspace_for(pro, *([s] * 7), 1, h, h, t, d, 0, offs, 4, None)
+
+    t = 1 << 20
+    assert exact(0, t, 8, 64) == 0
+    big = exact(0, t, 64, 64)
+    assert big == t * 64 * 2 * 4 * 4                          # fp32 (p, dS) per row and slot
+    assert lib.sbda_backward_workspace(1, 64, 64, t, 64, 0, offs, 4, None) >= big
+    assert lib.sbda_backward_workspace(1, 8, 8, t, 64, 0, offs, 4, None) >= exact(0, t, 8, 64)
+    for h in (8, 64):
+        assert 0 < exact(1, t, h, 64) <= lib.sbda_backward_prologue_workspace(1, h, h, t, 64, 0,
+                                                                               offs, 4, None)
+    bad = lib.sbda_backward_workspace_for(0, *([strides(t, 8, 64)] * 7), 1, 8, 8, t, 64, 7, offs,
+                                          4, None)
+    assert bad < 0                                            # unknown dtype code
+
+
 def test_outputs_keep_the_inputs_position_major_layout():
     # Outputs and gradients are allocated dense in the input's stride order:
     # [B,T,H,D] memory seen as [B,H,T,D] (the reference's empty_like(q)), a

@@ -330,20 +330,10 @@ def test_chained_prologue_backward_wide_row_stride():
 
 # --------------------------------------------------- metric-size properties
 
-@pytest.mark.parametrize("layer", [3, 20])
-def test_metric_shape_sampled_rows(layer):
-    # T = 2**20, H = 8, D = 64 bf16: check 2048 sampled rows of the output and
-    # of each gradient against the oracle evaluated on those rows' sources.
-    t, h, d = 1 << 20, 8, 64
-    offs = ref.sbda_layer_offsets(layer)
-    gen = torch.Generator(device=DEV).manual_seed(500 + layer)
-    q, k, v, g = (torch.randn(1, t, h, d, generator=gen, device=DEV).to(torch.bfloat16) for _ in range(4))
-    qd, kd, vd = (x.permute(0, 2, 1, 3).requires_grad_() for x in (q, k, v))
-    out = sbda_amd.fused_sbda_key_backward(qd, kd, vd, torch.tensor(offs, dtype=torch.int32, device=DEV))
-    out.backward(g.permute(0, 2, 1, 3))
-    torch.cuda.synchronize()
-    rows = torch.cat([torch.arange(0, 8), torch.randint(0, t, (2040,), generator=torch.Generator().manual_seed(3))])
-    rows = rows.unique()
+def _check_sampled_rows(q, k, v, g, offs, out, dq_, dk_, dv_, rows):
+    """Rows ``rows`` of out and of each gradient ([B=1,H,T,D] views) against
+    the oracle evaluated on those rows' sources (q/k/v/g: [1, T, H, D])."""
+    t, h, d = q.shape[1], q.shape[2], q.shape[3]
     qf, kf, vf, gf = (x[0].float().cpu() for x in (q, k, v, g))   # [T, H, D]
     scale = d ** -0.5
 
@@ -356,9 +346,9 @@ def test_metric_shape_sampled_rows(layer):
         return js, ok, torch.softmax(sc, 0)
 
     got_o = out.detach()[0].permute(1, 0, 2).float().cpu()
-    got_dq = qd.grad[0].permute(1, 0, 2).float().cpu()
-    got_dk = kd.grad[0].permute(1, 0, 2).float().cpu()
-    got_dv = vd.grad[0].permute(1, 0, 2).float().cpu()
+    got_dq = dq_[0].permute(1, 0, 2).float().cpu()
+    got_dk = dk_[0].permute(1, 0, 2).float().cpu()
+    got_dv = dv_[0].permute(1, 0, 2).float().cpu()
 
     def dS(i):
         js, ok, p = weights(i)
@@ -380,6 +370,43 @@ def test_metric_shape_sampled_rows(layer):
                 dv += pq[s][:, None] * gf[qi]
         for name, a, w in (("out", got_o[i], o), ("dq", got_dq[i], dq), ("dk", got_dk[i], dk), ("dv", got_dv[i], dv)):
             torch.testing.assert_close(a, w, **LOW_TOL, msg=lambda m: f"row {i} {name}: {m}")
+
+
+@pytest.mark.parametrize("layer", [3, 20])
+def test_metric_shape_sampled_rows(layer):
+    # T = 2**20, H = 8, D = 64 bf16: check 2048 sampled rows of the output and
+    # of each gradient against the oracle evaluated on those rows' sources.
+    t, h, d = 1 << 20, 8, 64
+    offs = ref.sbda_layer_offsets(layer)
+    gen = torch.Generator(device=DEV).manual_seed(500 + layer)
+    q, k, v, g = (torch.randn(1, t, h, d, generator=gen, device=DEV).to(torch.bfloat16) for _ in range(4))
+    qd, kd, vd = (x.permute(0, 2, 1, 3).requires_grad_() for x in (q, k, v))
+    out = sbda_amd.fused_sbda_key_backward(qd, kd, vd, torch.tensor(offs, dtype=torch.int32, device=DEV))
+    out.backward(g.permute(0, 2, 1, 3))
+    torch.cuda.synchronize()
+    rows = torch.cat([torch.arange(0, 8), torch.randint(0, t, (2040,), generator=torch.Generator().manual_seed(3))])
+    _check_sampled_rows(q, k, v, g, offs, out, qd.grad, kd.grad, vd.grad, rows.unique())
+
+
+@pytest.mark.parametrize("layer", [3, 20])
+def test_row_span_past_4_gib_runs_generic_kernels(layer):
+    # q, k, v and grad_out are 8-head slices of one [1, 2^20, 64, 64] bf16
+    # buffer: an 8 KiB position stride, so a head group spans 8 GiB -- past the
+    # walk kernels' 32-bit offsets.  The generic kernels run, with the
+    # workspace the stride-aware query sizes.
+    t, d = 1 << 20, 64
+    offs = ref.sbda_layer_offsets(layer)
+    gen = torch.Generator(device=DEV).manual_seed(700 + layer)
+    buf = torch.randn(1, t, 64, d, generator=gen, device=DEV).to(torch.bfloat16)
+    q, k, v, g = (buf[:, :, 8 * i:8 * i + 8] for i in range(4))
+    qd, kd, vd = (x.permute(0, 2, 1, 3).detach().requires_grad_() for x in (q, k, v))
+    out = sbda_amd.fused_sbda_key_backward(qd, kd, vd, torch.tensor(offs, dtype=torch.int32, device=DEV))
+    out.backward(g.permute(0, 2, 1, 3))
+    torch.cuda.synchronize()
+    rows = torch.cat([torch.arange(0, 4), torch.tensor([t - 1]),
+                      torch.randint(0, t, (400,), generator=torch.Generator().manual_seed(5))])
+    _check_sampled_rows(q, k, v, g, offs, out, qd.grad, kd.grad, vd.grad, rows.unique())
+    del buf
 
 
 def test_rope_table_matches_fp32_reference_angles():

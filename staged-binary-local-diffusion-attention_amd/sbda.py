@@ -57,6 +57,10 @@ def host_offsets(offsets) -> tuple[int, ...]:
     if isinstance(offsets, torch.Tensor):
         if offsets.ndim != 1:
             raise ValueError("offsets must be a 1-D tensor")
+        if offsets.is_inference():
+            # Inference tensors keep no version counter (and may change in
+            # place inside inference mode): read them every time.
+            return tuple(int(x) for x in offsets.detach().to("cpu", torch.int64).tolist())
         key = id(offsets)
         hit = _OFFSET_CACHE.get(key)
         if hit is not None and hit[0]() is offsets and hit[1] == offsets._version:

@@ -105,6 +105,11 @@ def test_host_offsets_cache():
     t[3] = 16                                   # bumps the version counter
     assert sbda_amd.host_offsets(t) == (0, 1, 2, 16)
     assert sbda_amd.host_offsets([0, 2]) == (0, 2)
+    with torch.inference_mode():                # no version counter: read each time
+        u = torch.tensor([0, 1, 2, 4], dtype=torch.int32)
+        assert sbda_amd.host_offsets(u) == (0, 1, 2, 4)
+        u[3] = 32
+        assert sbda_amd.host_offsets(u) == (0, 1, 2, 32)
 
 
 def test_backward_workspace_queries():

@@ -1119,12 +1119,197 @@ __global__ __launch_bounds__(256) void bwd_fix_pro(Params p, ChainCfg c, int64_t
   write_group_partials<T, LPR, 1>(dw, red, 4, parts, part0 + blockIdx.x, p.D);
 }
 
+// ---- forward as row chains (far offsets F >= 16 in column order)
+//
+// The workgroup's waves walk W consecutive rows of one column band in
+// lockstep (one barrier per step, as the chained backwards): wave w publishes
+// its roped k and raw v rows in LDS and wave w + 1 takes them as its far-left
+// sources in the same step, so only the first wave of a chain loads and ropes
+// far rows.  Rows past the end walk clamped rows and store nothing.
+
+template <int VEC>
+struct FwdChainSlot {
+  float4 kf[2][VEC / 4][64];   // [t & 1][quarter][lane]: roped k of position t
+  u32x4 vf[2][64];             // [t & 1][lane]: raw v
+};
+
+template <typename T, int LPR, int NM, bool LEFT_LDS>
+struct FwdChainPro : ProBase<T, LPR> {
+  using B_ = ProBase<T, LPR>;
+  using B_::VEC;
+  using B_::HV;
+  using Slot = FwdChainSlot<VecOf<T>::value>;
+  static constexpr int NN = NearSet<NM>::count;
+  static constexpr int NS = NN + 1;
+
+  SplitStream q, k, v, o;
+  Stream lse;
+  int F, lane;
+  float scale;
+  Slot* mine;
+  const Slot* up;
+  Raw kraw[2], qraw[2], vraw[2], klr[2], vlr[2];
+  float cc[2][HV], ss[2][HV], clc[2][HV], cls[2][HV];
+  float kq[4][VEC], vr[4][VEC];
+
+  template <int R>
+  __device__ inline void prefetch(int t) {
+    const int tc = clampi(t, this->Tm1);
+    kraw[R & 1] = load_split(k, tc);
+    qraw[R & 1] = load_split(q, tc);
+    vraw[R & 1] = load_split(v, tc);
+    this->cs(tc, cc[R & 1], ss[R & 1]);
+    if constexpr (!LEFT_LDS) {
+      const int tf = clampi(t - F, this->Tm1);
+      klr[R & 1] = load_split(k, tf);
+      vlr[R & 1] = load_split(v, tf);
+      this->cs(tf, clc[R & 1], cls[R & 1]);
+    }
+  }
+
+  template <int R>
+  __device__ inline void compute(int t, bool store) {
+    this->rope(kraw[R & 1], this->wk, cc[R & 1], ss[R & 1], kq[R]);
+    widen<T>(vraw[R & 1], vr[R]);
+    put_rows<VEC>(mine->kf[R & 1], lane, kq[R]);
+    mine->vf[R & 1][lane] = pack_raw(vraw[R & 1]);
+    float qr[VEC];
+    this->rope(qraw[R & 1], this->wq, cc[R & 1], ss[R & 1], qr);
+    __syncthreads();
+    float kf[VEC], vf[VEC];
+    if constexpr (LEFT_LDS) {
+      get_rows<VEC>(up->kf[R & 1], lane, kf);
+      widen<T>(unpack_raw(up->vf[R & 1][lane]), vf);
+    } else {
+      this->rope(klr[R & 1], this->wk, clc[R & 1], cls[R & 1], kf);
+      widen<T>(vlr[R & 1], vf);
+    }
+    float sc[NS];
+    bool ok[NS];
+    int idx = 0;
+#pragma unroll
+    for (int n = 0; n < 3; ++n) {
+      if (NM & (1 << n)) {
+        ok[idx] = t - n >= 0;
+        sc[idx] = row_sum<LPR>(dot_partial<VEC>(qr, kq[(R + 4 - n) & 3])) * scale;
+        ++idx;
+      }
+    }
+    ok[NS - 1] = t - F >= 0;
+    sc[NS - 1] = row_sum<LPR>(dot_partial<VEC>(qr, kf)) * scale;
+    float m = -INFINITY;
+#pragma unroll
+    for (int s_ = 0; s_ < NS; ++s_) m = ok[s_] ? fmaxf(m, sc[s_]) : m;
+    float w[NS], l = 0.f;
+#pragma unroll
+    for (int s_ = 0; s_ < NS; ++s_) {
+      w[s_] = ok[s_] ? fast_exp(sc[s_] - m) : 0.f;
+      l += w[s_];
+    }
+    float acc[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+    idx = 0;
+#pragma unroll
+    for (int n = 0; n < 3; ++n) {
+      if (NM & (1 << n)) {
+        const int slot = (R + 4 - n) & 3;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] = __builtin_fmaf(w[idx], vr[slot][e], acc[e]);
+        ++idx;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = __builtin_fmaf(w[NS - 1], vf[e], acc[e]);
+    // l >= 1 whenever a source is valid (the largest term is exp(0)).
+    const float inv = l > 0.f ? __builtin_amdgcn_rcpf(l) : 0.f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] *= inv;
+    if (store) {
+      store_split<T>(o, t, acc);
+      if (this->li == 0) store_f32(lse, t, l > 0.f ? m + fast_log(l) : INFINITY);
+    }
+  }
+};
+
+template <typename T, int LPR, int NM, bool LEFT_LDS, int W>
+__device__ inline void fwd_chain_wave(const Params& p, const ChainCfg& c,
+                                      FwdChainSlot<VecOf<T>::value>* lds, int w, int b, int hg,
+                                      int a) {
+  constexpr int esz = (int)sizeof(T);
+  const int lane = threadIdx.x & 63, hl = lane / LPR, li = lane % LPR;
+  const int h0 = hg * (64 / LPR);
+  FwdChainPro<T, LPR, NM, LEFT_LDS> x;
+  x.init(p, li);
+  x.q = make_split(p.q, esz, b, h0, hl, li, p.D, x.HV);
+  x.k = make_split(p.k, esz, b, h0, hl, li, p.D, x.HV);
+  x.v = make_split(p.v, esz, b, h0, hl, li, p.D, x.HV);
+  x.o = make_split(p.o, esz, b, h0, hl, li, p.D, x.HV);
+  x.lse = lse_stream(p, b, h0, hl);
+  x.scale = p.scale;
+  x.F = c.F;
+  x.lane = lane;
+  x.mine = lds + w;
+  x.up = lds + (LEFT_LDS ? w - 1 : w);
+  const int end = min(a + c.P, p.T);
+  // t = a-2 .. a+P-1 in steps of 4 (slot of t is (t - a + 2) & 3); the trip
+  // count depends only on P.
+  const int t0 = a - 2;
+  x.template prefetch<0>(t0);
+  for (int t = t0; t < a + c.P; t += 4) {
+    x.template prefetch<1>(t + 1);
+    x.template compute<0>(t, t >= a && t < end);
+    x.template prefetch<2>(t + 2);
+    x.template compute<1>(t + 1, t + 1 >= a && t + 1 < end);
+    x.template prefetch<3>(t + 3);
+    x.template compute<2>(t + 2, t + 2 >= a && t + 2 < end);
+    x.template prefetch<0>(t + 4);
+    x.template compute<3>(t + 3, t + 3 >= a && t + 3 < end);
+  }
+}
+
+template <typename T, int LPR, int NM, int W>
+__global__ __launch_bounds__(64 * W) void fwd_chain_pro(Params p, ChainCfg c) {
+  __shared__ FwdChainSlot<VecOf<T>::value> lds[W];
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  // Workgroup -> (batch, head group, band, row block), XCD-contiguous; wave w
+  // -> row w of the block.
+  int64_t g = xcd_remap(blockIdx.x, gridDim.x);
+  const int rb = (int)(g % c.blocks);
+  g /= c.blocks;
+  const int cb = (int)(g % c.bands);
+  g /= c.bands;
+  const int hg = (int)(g % c.HG);
+  const int b = (int)(g / c.HG);
+  const int r = rb * W + w;
+  const int64_t a64 = (int64_t)r * c.F + (int64_t)cb * c.P;
+  const int a = (r < c.rows && a64 < p.T) ? (int)a64 : p.T;
+  if (w == 0)
+    fwd_chain_wave<T, LPR, NM, false, W>(p, c, lds, w, b, hg, a);
+  else
+    fwd_chain_wave<T, LPR, NM, true, W>(p, c, lds, w, b, hg, a);
+}
+
 }  // namespace
 
 template <typename T, int LPR, int NM, bool FAR>
 hipError_t pro_pattern(bool fwd, const Params& p, const WalkCfg& c, int dtype, hipStream_t st) {
   const dim3 grid((unsigned)c.nwg), block(kPipeBlock);
   if (fwd) {
+    if constexpr (FAR) {
+      if (c.column) {
+        const ChainCfg cc = make_chain_cfg(p.B, p.q.st * (int64_t)sizeof(T), c);
+        if (cc.nwg <= 0) return hipErrorInvalidValue;
+        const dim3 cgrid((unsigned)cc.nwg), cblock(64 * cc.W);
+        switch (cc.W) {
+          case 8: hipLaunchKernelGGL((fwd_chain_pro<T, LPR, NM, 8>), cgrid, cblock, 0, st, p, cc); break;
+          case 4: hipLaunchKernelGGL((fwd_chain_pro<T, LPR, NM, 4>), cgrid, cblock, 0, st, p, cc); break;
+          case 2: hipLaunchKernelGGL((fwd_chain_pro<T, LPR, NM, 2>), cgrid, cblock, 0, st, p, cc); break;
+          default: hipLaunchKernelGGL((fwd_chain_pro<T, LPR, NM, 1>), cgrid, cblock, 0, st, p, cc); break;
+        }
+        return hipGetLastError();
+      }
+    }
     hipLaunchKernelGGL((fwd_pipe_pro<T, LPR, NM, FAR>), grid, block, kPipeLds, st, p, c);
     return hipGetLastError();
   }

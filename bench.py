@@ -177,7 +177,8 @@ def other_configs(torch, sbda, dev) -> dict:
         "ms": ms, "tokens_per_s": (1 << 20) / (ms * 1e-3),
         "note": "BiAttnLM.forward_hidden, 20 layers, d=512, 8x64 heads, FFN 2048, bf16, "
                 "T=2^20, vocab head excluded; attention = fused norm+RoPE+SBDA kernels, "
-                "projections/FFN = torch (hipBLASLt)"}
+                "gate/up projection + SwiGLU = one MFMA kernel, q/k/v, out and down "
+                "projections = torch (hipBLASLt)"}
     del model, ids
     return res
 

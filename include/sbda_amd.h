@@ -276,6 +276,24 @@ int sbda_swiglu_backward(const void* dout, const void* gate_up, void* dgate_up, 
                          int64_t hidden, int32_t dtype, void* stream);
 
 /*
+ * Gate/up projection with the SwiGLU activation in its epilogue (replaces
+ * `F.silu(self.gate(x)) * self.up(x)`, BiAttn/model.py:32-59, as one MFMA
+ * GEMM kernel; no autograd state is kept):
+ *   out[r, j] = silu(g) * u,  g = x[r] . weight[j] + bias[j],
+ *                             u = x[r] . weight[hidden + j] + bias[hidden + j]
+ * x [rows, dim], weight [2 * hidden, dim] (gate rows, then up rows), out
+ * [rows, hidden], all row-major in `dtype` (bf16 or fp16 only); bias is fp32
+ * [2 * hidden] or NULL.  g and u are rounded to the dtype before the
+ * activation, silu(g) after it.  Shapes: dim a multiple of 64, hidden a
+ * multiple of 128, rows * dim and 2 * hidden * dim below 2^31
+ * (sbda_swiglu_gemm_supported).  Buffers 16-byte aligned.
+ */
+int sbda_swiglu_gemm_supported(int64_t rows, int64_t dim, int64_t hidden, int32_t dtype);
+int sbda_swiglu_gemm_forward(const void* x, const void* weight, const float* bias, void* out,
+                             int64_t rows, int64_t dim, int64_t hidden, int32_t dtype,
+                             void* stream);
+
+/*
  * RoPE tables: cos/sin[t, i] = cos/sin(fl32(t * inv_freq[i])) for t < length,
  * i < head_dim/2, as fp32 [length, head_dim/2].  inv_freq is a host fp32
  * array of head_dim/2 values (head_dim <= 512).

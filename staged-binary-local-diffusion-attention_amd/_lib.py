@@ -11,7 +11,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("libsbda_amd.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 OK, ERR_VALUE, ERR_DTYPE, ERR_RUNTIME = 0, 1, 2, 3
 _ERRORS = {ERR_VALUE: ValueError, ERR_DTYPE: TypeError, ERR_RUNTIME: RuntimeError}
@@ -65,6 +65,8 @@ SIGNATURES = {
                                              _i64, _i32, _p]),
     "sbda_swiglu_forward": (ctypes.c_int, [_p, _p, _i64, _i64, _i32, _p]),
     "sbda_swiglu_backward": (ctypes.c_int, [_p, _p, _p, _i64, _i64, _i32, _p]),
+    "sbda_swiglu_gemm_supported": (ctypes.c_int, [_i64, _i64, _i64, _i32]),
+    "sbda_swiglu_gemm_forward": (ctypes.c_int, [_p, _p, _fptr, _p, _i64, _i64, _i64, _i32, _p]),
     "sbda_rope_table": (ctypes.c_int, [_p, _p, ctypes.POINTER(ctypes.c_float), _i64, _i64, _p]),
 }
 

@@ -10,7 +10,11 @@ activation.  Here they are HIP kernels (``csrc/sbda_block.hip``):
   from its other uses;
 * :func:`fused_rms_norm` -- ``rms_norm(x)`` alone;
 * :func:`fused_swiglu` -- ``silu(gate) * up`` on the output of one
-  ``[gate | up]`` GEMM.
+  ``[gate | up]`` GEMM;
+* :func:`fused_swiglu_gemm` -- the ``[gate | up]`` GEMM itself with the
+  activation in its epilogue (an MFMA kernel, ``csrc/sbda_ffn.hip``), for
+  calls that need no gradient: the ``[T, 2 * hidden]`` product is never
+  written.
 
 Device tensors only; errors follow the attention ops' classes.
 """
@@ -137,4 +141,46 @@ def fused_swiglu(gate_up: torch.Tensor) -> torch.Tensor:
     return _SwiGLU.apply(gate_up)
 
 
-__all__ = ["fused_add_rms_norm", "fused_rms_norm", "fused_swiglu"]
+def swiglu_gemm_supported(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    """Whether :func:`fused_swiglu_gemm` takes these operands (device bf16 or
+    fp16, ``dim`` a multiple of 64, ``hidden`` a multiple of 128)."""
+    if not (x.is_cuda and weight.is_cuda) or x.dtype != weight.dtype:
+        return False
+    if x.dtype not in (torch.bfloat16, torch.float16) or weight.ndim != 2:
+        return False
+    dim = x.shape[-1]
+    if weight.shape[1] != dim or weight.shape[0] % 2:
+        return False
+    rows = x.numel() // dim if dim else 0
+    return bool(_lib.load().sbda_swiglu_gemm_supported(rows, dim, weight.shape[0] // 2,
+                                                        _DTYPES[x.dtype]))
+
+
+def fused_swiglu_gemm(x: torch.Tensor, weight: torch.Tensor,
+                      bias: torch.Tensor | None = None) -> torch.Tensor:
+    """``silu(x @ Wg.T + bg) * (x @ Wu.T + bu)`` for ``weight = [Wg; Wu]``
+    (``[2 * hidden, dim]``) as one HIP kernel.  No autograd graph is
+    recorded: call it where no gradient is needed (inference, ``no_grad``)."""
+    if not swiglu_gemm_supported(x, weight):
+        raise ValueError("fused_swiglu_gemm: unsupported operands (device bf16/fp16, dim a "
+                         "multiple of 64, hidden a multiple of 128)")
+    dim = x.shape[-1]
+    hidden = weight.shape[0] // 2
+    xs = _rows(x.detach(), dim)
+    ws = _rows(weight.detach(), dim)
+    b32 = None
+    if bias is not None:
+        if bias.shape != (2 * hidden,):
+            raise ValueError("bias must have shape [2 * hidden]")
+        b32 = bias.detach().to(device=x.device, dtype=torch.float32).contiguous()
+    rows = xs.numel() // dim
+    out = torch.empty(*xs.shape[:-1], hidden, dtype=xs.dtype, device=xs.device)
+    lib = _lib.load()
+    with _on_device(x.device):
+        _lib.check(lib.sbda_swiglu_gemm_forward(_ptr(xs), _ptr(ws), _ptr(b32), _ptr(out), rows,
+                                                dim, hidden, _DTYPES[xs.dtype], _stream(xs)))
+    return out
+
+
+__all__ = ["fused_add_rms_norm", "fused_rms_norm", "fused_swiglu", "fused_swiglu_gemm",
+           "swiglu_gemm_supported"]

@@ -36,6 +36,9 @@ hipError_t swiglu_forward(const void* gu, void* h, int64_t rows, int hidden, int
                           hipStream_t st);
 hipError_t swiglu_backward(const void* dh, const void* gu, void* dgu, int64_t rows, int hidden,
                            int dtype, hipStream_t st);
+bool ffn_swiglu_supported(int64_t rows, int64_t dim, int64_t hidden, int dtype);
+hipError_t ffn_swiglu_forward(const void* x, const void* w, const float* bias, void* h,
+                              int64_t rows, int dim, int hidden, int dtype, hipStream_t st);
 
 namespace {
 
@@ -370,7 +373,7 @@ using namespace sbda;
 
 extern "C" {
 
-int sbda_abi_version(void) { return 8; }
+int sbda_abi_version(void) { return 9; }
 
 const char* sbda_last_error(void) { return g_error.c_str(); }
 
@@ -585,6 +588,29 @@ int sbda_swiglu_backward(const void* dout, const void* gate_up, void* dgate_up, 
   return hip_status(swiglu_backward(dout, gate_up, dgate_up, rows, (int)hidden, dtype,
                                     reinterpret_cast<hipStream_t>(stream)),
                     "sbda swiglu backward launch");
+}
+
+int sbda_swiglu_gemm_supported(int64_t rows, int64_t dim, int64_t hidden, int32_t dtype) {
+  return ffn_swiglu_supported(rows, dim, hidden, dtype) ? 1 : 0;
+}
+
+int sbda_swiglu_gemm_forward(const void* x, const void* weight, const float* bias, void* out,
+                             int64_t rows, int64_t dim, int64_t hidden, int32_t dtype,
+                             void* stream) {
+  g_error.clear();
+  if (dtype != kBF16 && dtype != kFP16)
+    return fail(SBDA_ERR_DTYPE, "swiglu gemm: dtype code %d (bf16 or fp16 only)", (int)dtype);
+  if (!x || !weight || !out) return fail(SBDA_ERR_VALUE, "swiglu gemm: null pointer");
+  if (!ffn_swiglu_supported(rows, dim, hidden, dtype))
+    return fail(SBDA_ERR_VALUE,
+                "swiglu gemm: unsupported shape rows=%lld dim=%lld hidden=%lld (dim a multiple "
+                "of 64, hidden a multiple of 128, rows*dim and 2*hidden*dim below 2^31)",
+                (long long)rows, (long long)dim, (long long)hidden);
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(out) || (bias && !aligned16(bias)))
+    return fail(SBDA_ERR_VALUE, "swiglu gemm: buffers must be 16-byte aligned");
+  return hip_status(ffn_swiglu_forward(x, weight, bias, out, rows, (int)dim, (int)hidden, dtype,
+                                       reinterpret_cast<hipStream_t>(stream)),
+                    "sbda swiglu gemm launch");
 }
 
 int sbda_rope_table(float* rope_cos, float* rope_sin, const float* inv_freq, int64_t length,

@@ -26,7 +26,8 @@ from torch import Tensor, nn
 from torch.nn import functional as F
 
 from .attention import SBDAttention
-from .block import fused_add_rms_norm, fused_rms_norm, fused_swiglu
+from .block import (fused_add_rms_norm, fused_rms_norm, fused_swiglu, fused_swiglu_gemm,
+                    swiglu_gemm_supported)
 
 
 class RMSNorm(nn.Module):
@@ -69,10 +70,14 @@ class SwiGLU(nn.Module):
     def forward(self, x: Tensor) -> Tensor:
         if not x.is_cuda:
             return self.dropout(self.down(F.silu(self.gate(x)) * self.up(x)))
-        # One [gate | up] GEMM, then silu(gate) * up in one HIP pass.
         weight = torch.cat((self.gate.weight, self.up.weight), dim=0)
         bias = (None if self.gate.bias is None
                 else torch.cat((self.gate.bias, self.up.bias), dim=0))
+        if not torch.is_grad_enabled() and swiglu_gemm_supported(x, weight):
+            # No gradient needed: the [gate | up] GEMM with the activation in
+            # its epilogue, one MFMA kernel.
+            return self.dropout(self.down(fused_swiglu_gemm(x, weight, bias)))
+        # One [gate | up] GEMM, then silu(gate) * up in one HIP pass.
         return self.dropout(self.down(fused_swiglu(F.linear(x, weight, bias))))
 
 

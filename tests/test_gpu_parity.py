@@ -907,6 +907,49 @@ def test_fused_swiglu_matches_fp32_reference(dtype, tol, hidden):
     torch.testing.assert_close(gud.grad.float().cpu(), guc.grad, **tol)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,dim,hidden,with_bias", [
+    (1, 64, 128, True),          # one token: a single, mostly clamped token tile
+    (257, 128, 384, False),      # ragged token tail, three hidden tiles, no bias
+    (300, 512, 256, True),
+    (1000, 2048, 128, True),     # 32 k stages
+    (4096, 512, 2048, True),     # the config-5 feed-forward shape (16 x 16 tiles)
+])
+def test_fused_swiglu_gemm_matches_fp32_reference(dtype, rows, dim, hidden, with_bias):
+    g = torch.Generator().manual_seed(rows + dim + hidden)
+    x = torch.randn(rows, dim, generator=g).to(dtype)
+    w = (torch.randn(2 * hidden, dim, generator=g) / math.sqrt(dim)).to(dtype)
+    b = (0.1 * torch.randn(2 * hidden, generator=g)).to(dtype) if with_bias else None
+    xd, wd = x.to(DEV), w.to(DEV)
+    bd = None if b is None else b.to(DEV)
+    assert sbda_amd.swiglu_gemm_supported(xd, wd)
+    got = sbda_amd.fused_swiglu_gemm(xd, wd, bd)
+    assert got.shape == (rows, hidden) and got.dtype == dtype
+    gu = x.float() @ w.float().t()
+    if b is not None:
+        gu = gu + b.float()
+    want = torch.nn.functional.silu(gu[:, :hidden]) * gu[:, hidden:]
+    torch.testing.assert_close(got.float().cpu(), want, **LOW_TOL)
+    # Against the unfused device path (GEMM rounded to the dtype, then the
+    # activation kernel): the same rounding points, so within two units in
+    # the last place.
+    unfused = sbda_amd.fused_swiglu(torch.nn.functional.linear(xd, wd, bd))
+    ulp = 2.0 ** (-7 if dtype == torch.bfloat16 else -10)
+    torch.testing.assert_close(got.float(), unfused.float(), rtol=2 * ulp, atol=1e-3)
+
+
+def test_swiglu_module_uses_the_fused_gemm_without_grad():
+    torch.manual_seed(3)
+    ff = sbda_amd.model.SwiGLU(512, 4.0, hidden_size=2048).to(device=DEV, dtype=torch.bfloat16)
+    x = torch.randn(3, 333, 512, device=DEV).to(torch.bfloat16)
+    with torch.no_grad():
+        fused = ff(x)
+    eager = ff(x.requires_grad_())              # the grad-recording path
+    eager.sum().backward()
+    assert fused.shape == eager.shape
+    torch.testing.assert_close(fused.float(), eager.detach().float(), rtol=2e-2, atol=2e-3)
+
+
 def test_bf16_backbone_tracks_the_fp32_oracle_composition():
     # The config-5 layer shape (d=512, 8 x 64 heads, FFN 2048) in bf16 on the
     # GPU -- fused QKV GEMM, add+RMSNorm and SwiGLU kernels -- against the same

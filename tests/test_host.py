@@ -218,3 +218,21 @@ def test_backbone_surface_matches_reference():
         sbda_amd.BiAttnConfig(vocab_size=32, attention_backend="left").validate()
     with pytest.raises(NotImplementedError, match="CPU tensor"):
         m(torch.tensor([[1, 2, 3]]))
+
+
+def test_swiglu_gemm_validation_without_launching():
+    lib = _lib.load()
+    ok = lib.sbda_swiglu_gemm_supported
+    assert ok(1 << 20, 512, 2048, 0) == 1 and ok(1, 64, 128, 1) == 1
+    assert ok(1 << 20, 512, 2048, 2) == 0          # fp32: no MFMA path
+    assert ok(100, 48, 128, 0) == 0                # dim not a multiple of 32
+    assert ok(100, 512, 200, 0) == 0               # hidden not a multiple of 128
+    assert ok(1 << 22, 1024, 128, 0) == 0          # rows * dim reaches 2^31
+    z = ctypes.c_void_p(0)
+    assert lib.sbda_swiglu_gemm_forward(z, z, None, z, 8, 64, 128, 2, z) == _lib.ERR_DTYPE
+    assert lib.sbda_swiglu_gemm_forward(z, z, None, z, 8, 64, 128, 0, z) == _lib.ERR_VALUE
+    assert "null" in lib.sbda_last_error().decode()
+    with pytest.raises(ValueError):
+        sbda_amd.fused_swiglu_gemm(torch.zeros(4, 64, dtype=torch.bfloat16),
+                                   torch.zeros(256, 64, dtype=torch.bfloat16))
+    assert not sbda_amd.swiglu_gemm_supported(torch.zeros(4, 64), torch.zeros(256, 64))

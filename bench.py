@@ -165,22 +165,25 @@ def other_configs(torch, sbda, dev) -> dict:
         "note": "B=4 T=32768 H=8 D=64 bf16, 15 layers, norm+RoPE fused, via autograd"}
     del q, k, v, go
     torch.cuda.empty_cache()
-    # Config 5: the SBDA backbone's forward_hidden (20 layers, d_model 512,
-    # 8 x 64 heads, FFN 2048, pre-RMSNorm, bf16, random init, vocab head
-    # excluded) on T=2^20 character ids.
+    res["config5_backbone_forward_hidden"] = backbone_forward(torch, sbda, dev, gen)
+    return res
+
+
+def backbone_forward(torch, sbda, dev, gen, reps: int = 3) -> dict:
+    """Config 5: the SBDA backbone's forward_hidden (20 layers, d_model 512,
+    8 x 64 heads, FFN 2048, pre-RMSNorm, bf16, random init, vocab head
+    excluded) on T=2^20 character ids; median of ``reps`` runs."""
     cfg = sbda.BiAttnConfig(vocab_size=256, dim=512, layers=20, heads=8, ff_hidden=2048)
     model = sbda.BiAttnLM(cfg).to(device=dev, dtype=torch.bfloat16).eval()
     ids = torch.randint(0, 256, (1, 1 << 20), generator=gen, device=dev)
     with torch.inference_mode():
-        ms = _median_ms(torch, lambda: model.forward_hidden(ids), reps=3)
-    res["config5_backbone_forward_hidden"] = {
-        "ms": ms, "tokens_per_s": (1 << 20) / (ms * 1e-3),
-        "note": "BiAttnLM.forward_hidden, 20 layers, d=512, 8x64 heads, FFN 2048, bf16, "
-                "T=2^20, vocab head excluded; attention = fused norm+RoPE+SBDA kernels, "
-                "gate/up projection + SwiGLU = one MFMA kernel, q/k/v, out and down "
-                "projections = torch (hipBLASLt)"}
+        ms = _median_ms(torch, lambda: model.forward_hidden(ids), reps=reps)
     del model, ids
-    return res
+    return {"ms": ms, "tokens_per_s": (1 << 20) / (ms * 1e-3),
+            "note": "BiAttnLM.forward_hidden, 20 layers, d=512, 8x64 heads, FFN 2048, bf16, "
+                    "T=2^20, vocab head excluded; attention = fused norm+RoPE+SBDA kernels, "
+                    "gate/up projection + SwiGLU = one MFMA kernel, q/k/v, out and down "
+                    "projections = torch (hipBLASLt)"}
 
 
 def main() -> int:
@@ -198,6 +201,9 @@ def main() -> int:
                     help="for rocprofv3 counter runs: one untimed-warmup-free step, no CPU "
                          "baseline, preceded by a 256 MiB device copy whose counter readings "
                          "calibrate FETCH_SIZE/WRITE_SIZE")
+    ap.add_argument("--backbone-only", action="store_true",
+                    help="run only config 5 (the backbone forward, one warm-up and one "
+                         "timed call) and print its JSON object; for rocprofv3 kernel traces")
     args = ap.parse_args()
     if args.profile_pass:
         args.steps, args.warmup, args.no_cpu_baseline = 1, 0, True
@@ -214,6 +220,11 @@ def main() -> int:
     sbda = load_package()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.backbone_only:
+        gen5 = torch.Generator(device=dev).manual_seed(99)
+        print(json.dumps({"config5_backbone_forward_hidden":
+                          backbone_forward(torch, sbda, dev, gen5, reps=1)}), flush=True)
+        return 0
     b, t, h, d, layers = args.batch, args.length, args.heads, args.head_dim, args.layers
     dtype = torch.bfloat16
     gen = torch.Generator(device=dev).manual_seed(2024)

@@ -18,9 +18,11 @@
 // Tiling (gfx950, bf16/fp16 MFMA v_mfma_f32_32x32x16, fp32 accumulators):
 //   * a workgroup (4 waves) owns 128 token rows x 128 hidden units, i.e. 128
 //     rows of x against 256 weight rows (128 gate + the matching 128 up);
-//   * K advances 32 at a time through two 24 KiB LDS stages; the next stage's
-//     global loads are in flight while the current one feeds the MFMAs;
-//   * 194 VGPRs and 48 KiB of LDS give two workgroups per CU (two waves per
+//   * K advances 32 at a time through two 24 KiB LDS stages; the global loads
+//     of stage k + 2 are in flight (in one of two register sets) while stage
+//     k feeds the MFMAs and stage k + 1 is written to LDS, and each stage's
+//     fragments are all read before its first MFMA;
+//   * 212 VGPRs and 48 KiB of LDS give two workgroups per CU (two waves per
 //     SIMD), so one workgroup's epilogue and stage waits overlap the other's
 //     MFMAs;
 //   * a wave owns 64 tokens x 64 hidden units of both gate and up, so the
@@ -90,12 +92,43 @@ __device__ inline float silu_fast(float g) {
   return g * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-g * kLog2e));
 }
 
+// The MFMAs of one stage: every fragment of both 16-wide k sub-steps is read
+// from LDS first, then the 16 MFMAs.
+template <typename T>
+__device__ __forceinline__ void stage_mma(const uint4* __restrict__ s, int wm, int wn, int l32,
+                                          int khalf, f32x16 (&acc_g)[2][2],
+                                          f32x16 (&acc_u)[2][2]) {
+  typedef typename Mfma<T>::v8 v8;
+  v8 fx[2][2], fg[2][2], fu[2][2];
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    const int c = 2 * sub + khalf;
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+      fx[sub][tb] = __builtin_bit_cast(v8, s[slot(wm * 64 + tb * 32 + l32, c)]);
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      const int rg = kTokTile + wn * 64 + hb * 32 + l32;
+      fg[sub][hb] = __builtin_bit_cast(v8, s[slot(rg, c)]);
+      fu[sub][hb] = __builtin_bit_cast(v8, s[slot(rg + kHidTile, c)]);
+    }
+  }
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) {
+        acc_g[tb][hb] = Mfma<T>::run(fg[sub][hb], fx[sub][tb], acc_g[tb][hb]);
+        acc_u[tb][hb] = Mfma<T>::run(fu[sub][hb], fx[sub][tb], acc_u[tb][hb]);
+      }
+}
+
 template <typename T>
 __global__ __launch_bounds__(kFfnThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void ffn_gate_up_swiglu(const T* __restrict__ x, const T* __restrict__ w,
                         const float* __restrict__ bias, T* __restrict__ h, int64_t rows,
                         int dim, int hidden, int h_tiles) {
-  typedef typename Mfma<T>::v8 v8;
   __shared__ uint4 lds[2][kLdsRows * kChunks];
 
   const int tid = threadIdx.x;
@@ -137,7 +170,6 @@ void ffn_gate_up_swiglu(const T* __restrict__ x, const T* __restrict__ w,
     src[i] = (uint32_t)(row * dim + chunk * 8);
     dst[i] = (uint32_t)slot(r, chunk);
   }
-  uint4 st[kLoadsPerThread];
 
   // Wave tile: tokens wm * 64 + [0, 64), hidden wn * 64 + [0, 64).
   const int wm = wave & 1;
@@ -152,49 +184,49 @@ void ffn_gate_up_swiglu(const T* __restrict__ x, const T* __restrict__ w,
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc_g[a][b][e] = acc_u[a][b][e] = 0.f;
 
+  // Two register sets (a0-a5, b0-b5; named registers, not arrays, so they
+  // stay out of scratch): the loads of stage k + 2 are in flight while stage
+  // k is computed and stage k + 1 (loaded one stage earlier) is stashed.  The
+  // trip count is even (dim is a multiple of 64); loads past the last stage
+  // re-read it (in bounds, never stashed into a stage that is computed).
+  static_assert(kLoadsPerThread == 6 && kTokLoads == 2, "six chunks: 2 token, 4 weight");
   const int nk = dim / kBK;
-#pragma unroll
-  for (int i = 0; i < kLoadsPerThread; ++i)
-    st[i] = *reinterpret_cast<const uint4*>((i < kTokLoads ? x : w) + src[i]);
-#pragma unroll
-  for (int i = 0; i < kLoadsPerThread; ++i) lds[0][dst[i]] = st[i];
+  uint4 a0, a1, a2, a3, a4, a5, b0, b1, b2, b3, b4, b5;
+#define FFN_LOAD(R, KT)                                                            \
+  {                                                                                \
+    const int k0_ = min((KT), nk - 1) * kBK;                                       \
+    R##0 = *reinterpret_cast<const uint4*>(x + src[0] + k0_);                      \
+    R##1 = *reinterpret_cast<const uint4*>(x + src[1] + k0_);                      \
+    R##2 = *reinterpret_cast<const uint4*>(w + src[2] + k0_);                      \
+    R##3 = *reinterpret_cast<const uint4*>(w + src[3] + k0_);                      \
+    R##4 = *reinterpret_cast<const uint4*>(w + src[4] + k0_);                      \
+    R##5 = *reinterpret_cast<const uint4*>(w + src[5] + k0_);                      \
+  }
+#define FFN_STASH(R, BUF)                                                          \
+  {                                                                                \
+    lds[BUF][dst[0]] = R##0;                                                       \
+    lds[BUF][dst[1]] = R##1;                                                       \
+    lds[BUF][dst[2]] = R##2;                                                       \
+    lds[BUF][dst[3]] = R##3;                                                       \
+    lds[BUF][dst[4]] = R##4;                                                       \
+    lds[BUF][dst[5]] = R##5;                                                       \
+  }
+  FFN_LOAD(a, 0);
+  FFN_STASH(a, 0);
+  FFN_LOAD(b, 1);
   __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    // The last stage re-fetches itself (in bounds, never read back) so the
-    // loop body has no branch around the staging registers.
-    {
-      const int k0 = (kt + 1 < nk ? kt + 1 : kt) * kBK;
-#pragma unroll
-      for (int i = 0; i < kLoadsPerThread; ++i)
-        st[i] = *reinterpret_cast<const uint4*>((i < kTokLoads ? x : w) + src[i] + k0);
-    }
-    const uint4* s = lds[buf];
-#pragma unroll
-    for (int sub = 0; sub < kBK / 16; ++sub) {
-      const int c = 2 * sub + khalf;
-      v8 bx[2], ag[2], au[2];
-#pragma unroll
-      for (int tb = 0; tb < 2; ++tb)
-        bx[tb] = __builtin_bit_cast(v8, s[slot(wm * 64 + tb * 32 + l32, c)]);
-#pragma unroll
-      for (int hb = 0; hb < 2; ++hb) {
-        const int rg = kTokTile + wn * 64 + hb * 32 + l32;
-        ag[hb] = __builtin_bit_cast(v8, s[slot(rg, c)]);
-        au[hb] = __builtin_bit_cast(v8, s[slot(rg + kHidTile, c)]);
-      }
-#pragma unroll
-      for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-        for (int hb = 0; hb < 2; ++hb) {
-          acc_g[tb][hb] = Mfma<T>::run(ag[hb], bx[tb], acc_g[tb][hb]);
-          acc_u[tb][hb] = Mfma<T>::run(au[hb], bx[tb], acc_u[tb][hb]);
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < kLoadsPerThread; ++i) lds[buf ^ 1][dst[i]] = st[i];
+  for (int kt = 0; kt < nk; kt += 2) {
+    FFN_LOAD(a, kt + 2);
+    stage_mma<T>(lds[0], wm, wn, l32, khalf, acc_g, acc_u);
+    FFN_STASH(b, 1);
+    __syncthreads();
+    FFN_LOAD(b, kt + 3);
+    stage_mma<T>(lds[1], wm, wn, l32, khalf, acc_g, acc_u);
+    FFN_STASH(a, 0);
     __syncthreads();
   }
+#undef FFN_LOAD
+#undef FFN_STASH
 
   // Epilogue: acc[e] holds hidden 8 (e / 4) + 4 khalf + e % 4 of the 32-unit
   // block and token l32 of the 32-token block.
@@ -235,12 +267,13 @@ void ffn_gate_up_swiglu(const T* __restrict__ x, const T* __restrict__ w,
 
 }  // namespace
 
-// Shapes the fused kernel takes: bf16/fp16, K a multiple of 32, the hidden
-// width a multiple of 128, 32-bit element offsets.
+// Shapes the fused kernel takes: bf16/fp16, K a multiple of 64 (the stage
+// loop takes two 32-wide stages per trip), the hidden width a multiple of
+// 128, 32-bit element offsets.
 bool ffn_swiglu_supported(int64_t rows, int64_t dim, int64_t hidden, int dtype) {
   if (dtype != kBF16 && dtype != kFP16) return false;
   if (rows <= 0 || dim <= 0 || hidden <= 0) return false;
-  if (dim % kBK || hidden % kHidTile) return false;
+  if (dim % (2 * kBK) || hidden % kHidTile) return false;
   if (rows * dim >= (int64_t(1) << 31) || 2 * hidden * dim >= (int64_t(1) << 31)) return false;
   if (rows * hidden >= (int64_t(1) << 40)) return false;
   const int64_t tiles = ((rows + kTokTile - 1) / kTokTile) * (hidden / kHidTile);

@@ -225,7 +225,7 @@ def test_swiglu_gemm_validation_without_launching():
     ok = lib.sbda_swiglu_gemm_supported
     assert ok(1 << 20, 512, 2048, 0) == 1 and ok(1, 64, 128, 1) == 1
     assert ok(1 << 20, 512, 2048, 2) == 0          # fp32: no MFMA path
-    assert ok(100, 48, 128, 0) == 0                # dim not a multiple of 32
+    assert ok(100, 96, 128, 0) == 0                # dim not a multiple of 64
     assert ok(100, 512, 200, 0) == 0               # hidden not a multiple of 128
     assert ok(1 << 22, 1024, 128, 0) == 0          # rows * dim reaches 2^31
     z = ctypes.c_void_p(0)

@@ -210,7 +210,8 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the op shards over batch/heads with no exchange; see DESIGN.md).",
+              "(every (batch, head) plane is independent, so the op would shard over "
+              "batch and heads with no exchange between GPUs).",
               file=sys.stderr)
         return 2
 

@@ -6,8 +6,10 @@ backward (dQ, dK, dV) of one synthetic q/k/v/dO set (N(0,1), seeded, bf16,
 [B, T, H, D] memory seen as [B, H, T, D] views, as BiAttn/left_v2.py:240-244
 passes them).  Inputs are resident in HBM before timing starts.
 
-Prints one JSON line: positions/s (value), achieved algorithmic HBM GB/s and
-its fraction of MI355X's 8 TB/s, per-entry-point kernel times measured with
+Prints one JSON line: positions/s (value) and its fraction of the roofline
+positions/s (a step moving only its algorithmic bytes at 8 TB/s), achieved
+algorithmic HBM GB/s and its fraction of MI355X's 8 TB/s, per-entry-point
+kernel times measured with
 HIP events on the launch stream, and the CPU baseline (the oracle's eager
 restatement of left_v2's gather path, fp32, timed on this host on a bounded
 sample).
@@ -42,6 +44,14 @@ def algorithmic_bytes(rows: int, d: int, esz: int) -> tuple[int, int]:
     fwd = rows * (4 * d * esz + 4)
     bwd = rows * (7 * d * esz + 4)
     return fwd, bwd
+
+
+def roofline_positions_per_s(h: int, d: int, layers: int, esz: int = 2) -> float:
+    """Positions/s of a step that moved only its algorithmic bytes at the HBM
+    peak: every position carries h rows through each layer's forward and
+    backward."""
+    fwd, bwd = algorithmic_bytes(h, d, esz)
+    return HBM_PEAK_GBS * 1e9 / ((fwd + bwd) * layers)
 
 
 def cpu_baseline(layers: int, h: int, d: int, seconds_target: float = 15.0) -> dict:
@@ -322,6 +332,8 @@ def main() -> int:
                    "layout": "[B,T,H,D] memory as [B,H,T,D] views"},
         "achieved_gbs": gbs,
         "hbm_fraction": gbs / HBM_PEAK_GBS,
+        "roofline_positions_per_s": roofline_positions_per_s(h, d, layers),
+        "positions_fraction": positions_s / roofline_positions_per_s(h, d, layers),
         "copy_peak_gbs": copy_gbs,
         "copy_fraction": gbs / copy_gbs,
         "forward_ms_per_layer": fwd_ms,

@@ -39,6 +39,9 @@ def test_algorithmic_bytes_are_the_metric_figures():
     total = 20 * (fwd + bwd)
     assert total == 237_565_378_560
     assert total / 8e12 * 1e3 == pytest.approx(29.70, abs=0.01)   # ms at 8 TB/s
+    # 226,560 bytes per position over the 20 layers: 35.31 M positions/s at 8 TB/s.
+    assert bench.roofline_positions_per_s(8, 64, 20) == pytest.approx(8e12 / 226_560)
+    assert bench.roofline_positions_per_s(8, 64, 20) / 1e6 == pytest.approx(35.31, abs=0.01)
 
 
 def test_timed_schedule_is_the_sbda_route(sbda):

@@ -149,10 +149,28 @@ def other_configs(torch, sbda, dev) -> dict:
                 sbda.sbda_forward(q, k, v, offs)
 
         b2b.append(_median_ms(torch, burst) * 1e3 / 20)
+    # The same 20 calls captured once in a HIP graph and replayed: no host work
+    # or launch gaps between the kernels.
+    graphed = []
+    for layer in range(1, 13):
+        offs = sbda_offsets(layer)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            sbda.sbda_forward(q, k, v, offs)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(20):
+                sbda.sbda_forward(q, k, v, offs)
+        graphed.append(_median_ms(torch, graph.replay) * 1e3 / 20)
+        del graph
     res["config2_forward_us_per_layer"] = {
-        "layers_1_to_12": per, "back_to_back_layers_1_to_12": b2b, "cache_resident": True,
+        "layers_1_to_12": per, "back_to_back_layers_1_to_12": b2b,
+        "graph_replay_layers_1_to_12": graphed, "cache_resident": True,
         "note": "B=8 T=4096 H=8 D=64 bf16 forward; first list: one call on an idle GPU "
-                "(includes the host-side call), second: 20 back-to-back calls / 20"}
+                "(includes the host-side call), second: 20 back-to-back calls / 20, third: "
+                "the 20 calls captured in one HIP graph, replay time / 20"}
     del q, k, v
     # Config 3: 15-layer fwd+bwd, B=4, T=32768, H=8, D=64, q/k head-RMSNorm +
     # RoPE(10000) fused into the kernels (weights 1), through autograd.

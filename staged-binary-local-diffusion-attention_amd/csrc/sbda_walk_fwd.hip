@@ -28,16 +28,33 @@ struct FwdPipe {
   Raw kl[2], vl[2];     // far source t - F (FR == 0)
   float vr[RD][VEC];    // widened v rotation
 
+  // Defined contents for slots a skipped load leaves stale.
+  __device__ inline void init() {
+#pragma unroll
+    for (int i = 0; i < RD; ++i) kr[i] = Raw{};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) vraw[i] = qn[i] = kl[i] = vl[i] = Raw{};
+  }
+
+  // Rows of position t.  A query row (and its far source) only for positions
+  // the tile stores (q_ok); k and v also for the warm-up positions before the
+  // tile, whose rows are the first queries' sources, but not past its end
+  // (kv_ok).  Both flags are wave-uniform; a skipped row leaves its slot
+  // stale, and only steps that store nothing read such a slot.
   template <int R>
-  __device__ inline void prefetch(int t) {
+  __device__ inline void prefetch(int t, bool q_ok, bool kv_ok) {
     const int tc = clampi(t, Tm1);
-    kr[R] = load_at<!FAR>(k, tc);
-    vraw[R & 1] = load_at<!FAR>(v, tc);
-    qn[R & 1] = load_at<!FAR>(q, tc);
-    if constexpr (FAR && FR == 0) {
-      const int tf = clampi(t - F, Tm1);
-      kl[R & 1] = load_at(k, tf);
-      vl[R & 1] = load_at(v, tf);
+    if (kv_ok) {
+      kr[R] = load_at<!FAR>(k, tc);
+      vraw[R & 1] = load_at<!FAR>(v, tc);
+    }
+    if (q_ok) {
+      qn[R & 1] = load_at<!FAR>(q, tc);
+      if constexpr (FAR && FR == 0) {
+        const int tf = clampi(t - F, Tm1);
+        kl[R & 1] = load_at(k, tf);
+        vl[R & 1] = load_at(v, tf);
+      }
     }
   }
 
@@ -108,7 +125,8 @@ struct FwdPipe {
   template <int R>
   __device__ inline void steps(int t, int a, int end) {
     if constexpr (R < RD) {
-      prefetch<(R + 1) % RD>(t + R + 1);
+      const int n = t + R + 1;
+      prefetch<(R + 1) % RD>(n, n >= a && n < end, n < end);
       compute<R>(t + R, t + R >= a && t + R < end);
       steps<R + 1>(t, a, end);
     }
@@ -138,7 +156,8 @@ __global__ __launch_bounds__(kPipeBlock) void fwd_pipe(Params p, WalkCfg c) {
   // position t is (t - t0) % RD.
   // The trip count depends only on P (same for every wave of the workgroup).
   const int t0 = a - (FR > 2 ? FR : 2);
-  w.template prefetch<0>(t0);
+  w.init();
+  w.template prefetch<0>(t0, false, t0 < end);
   for (int t = t0; t < a + c.P; t += W::RD) {
     __syncthreads();
     w.template steps<0>(t, a, end);

@@ -8,7 +8,7 @@ What is restated, and from where (paths relative to the reference checkout):
 * ``sbda_layer_offsets``      -- ``BiAttn/topology.py:13-21,37-38,65-66``
 * ``path_tables``             -- ``BiAttn/left_v2.py:165-189``
 * ``head_rmsnorm``            -- ``BiAttn/attention_common.py:64-76``
-* ``rope_tables`` / ``apply_rope`` -- ``BiAttn/attention_common.py:8-50``
+* ``rope_tables`` / ``rotate_half`` / ``apply_rope`` -- ``BiAttn/attention_common.py:8-50``
 * ``gather_attention``        -- ``BiAttn/left_v2.py:313-405`` (both the
   matmul route ``use_sdpa=True`` and the elementwise route)
 * ``attention_lse``           -- the log-normaliser of the softmax in
@@ -134,43 +134,53 @@ def rope_inverse_frequencies(head_dim: int, theta: float) -> Tensor:
 
 
 def rope_tables(length: int, head_dim: int, theta: float,
-                dtype: torch.dtype) -> tuple[Tensor, Tensor]:
+                dtype: torch.dtype, positions: Tensor | None = None) -> tuple[Tensor, Tensor]:
     """``cos, sin`` of shape ``[length, head_dim]`` (``attention_common.py:13-22``).
 
     Angles are the fp32 product ``position * inverse_frequency``; each half
     of the last dim repeats the same ``D/2`` angles; the tables are cast to
-    the activation dtype.
+    the activation dtype.  Positions are ``0 .. length-1`` unless given
+    (the reference's ``q_positions`` / ``k_positions``, ``:31-46``).
     """
     inv = rope_inverse_frequencies(head_dim, theta)
-    ang = torch.outer(torch.arange(length).to(torch.float32), inv)
+    pos = torch.arange(length) if positions is None else positions
+    ang = torch.outer(pos.to(torch.float32), inv)
     cos = torch.cat((ang.cos(), ang.cos()), dim=-1).to(dtype)
     sin = torch.cat((ang.sin(), ang.sin()), dim=-1).to(dtype)
     return cos, sin
 
 
-def apply_rope(x: Tensor, theta: float) -> Tensor:
+def rotate_half(x: Tensor) -> Tensor:
+    """``cat(-x2, x1)`` over the last dim (``attention_common.py:8-10``)."""
+    half = x.shape[-1] // 2
+    return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+
+
+def apply_rope(x: Tensor, theta: float, positions: Tensor | None = None) -> Tensor:
     """Half-split RoPE of ``x`` laid out ``[B, T, H, D]`` (``attention_common.py:25-50``).
 
-    ``x * cos + rotate_half(x) * sin`` with ``rotate_half(x) = cat(-x2, x1)``;
-    odd ``D`` is the identity (``:36-40``).
+    ``x * cos + rotate_half(x) * sin`` (``:48-49``): each pair
+    ``(x[d], x[d + D/2])`` at position m is rotated by ``+m * inv_freq[d]``;
+    odd ``D`` is the identity (``:36-40``).  ``positions`` (``[T]``) are the
+    positions of the T rows, ``0 .. T-1`` by default (``:41-44``).
     """
     d = x.shape[-1]
     if d % 2:
         return x
-    cos, sin = rope_tables(x.shape[1], d, theta, x.dtype)
+    cos, sin = rope_tables(x.shape[1], d, theta, x.dtype, positions)
     cos = cos[None, :, None, :]
     sin = sin[None, :, None, :]
-    half = d // 2
-    rotated = torch.cat((-x[..., half:], x[..., :half]), dim=-1)
-    return x * cos + rotated * sin
+    return x * cos + rotate_half(x) * sin
 
 
 def prologue(q_raw: Tensor, k_raw: Tensor, q_weight: Tensor, k_weight: Tensor,
-             theta: float, eps: float = 1e-6) -> tuple[Tensor, Tensor]:
-    """``left_v2.py:237-239`` on ``[B, T, H, D]`` inputs: norm, then RoPE."""
+             theta: float, eps: float = 1e-6,
+             positions: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """``left_v2.py:237-239`` on ``[B, T, H, D]`` inputs: norm, then RoPE
+    (rows at ``positions``, ``0 .. T-1`` by default)."""
     qn = head_rmsnorm(q_raw, q_weight, eps)
     kn = head_rmsnorm(k_raw, k_weight, eps)
-    return apply_rope(qn, theta), apply_rope(kn, theta)
+    return apply_rope(qn, theta, positions), apply_rope(kn, theta, positions)
 
 
 # --------------------------------------------------------------------------

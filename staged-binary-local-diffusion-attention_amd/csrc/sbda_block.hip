@@ -121,7 +121,7 @@ __global__ __launch_bounds__(kNormBlock) void rmsnorm_fwd(const T* __restrict__ 
 #pragma unroll
         for (int i = 0; i < VEC; ++i) ss = __builtin_fmaf(v[u][c][i], v[u][c][i], ss);
       ss = row_sum<64>(ss);
-      const float rs = __builtin_amdgcn_rsqf(__fadd_rn(__fdiv_rn(ss, (float)dim), eps));
+      const float rs = norm_rsqrt<T>(__fadd_rn(__fdiv_rn(ss, (float)dim), eps));
       if (row < rows) {
 #pragma unroll
         for (int c = 0; c < C; ++c) {

@@ -175,6 +175,16 @@ __device__ inline float dot_partial(const float (&a)[VEC], const float (&b)[VEC]
   return s;
 }
 
+// rsqrt(mean(x^2) + eps) of an RMS norm.  fp32 rows: 1 / sqrt(x) with both
+// steps correctly rounded (what torch.rsqrt on fp32 CPU tensors gives to 1
+// ulp), so the fp32 path meets a 1e-5 relative bar; 16-bit rows: the hardware
+// approximation (~1 ulp, far below their own rounding).
+template <typename T>
+__device__ inline float norm_rsqrt(float x) {
+  if constexpr (sizeof(T) == 4) return __fdiv_rn(1.f, __fsqrt_rn(x));
+  else return __builtin_amdgcn_rsqf(x);
+}
+
 // exp(x) through the hardware exp2; exp(-inf) = 0.
 __device__ inline float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
 __device__ inline float fast_log(float x) { return __builtin_amdgcn_logf(x) * kLn2; }
@@ -228,7 +238,7 @@ struct Prologue {
 #pragma unroll
     for (int i = 0; i < VEC; ++i) ss = __builtin_fmaf(x[i], x[i], ss);
     ss = row_sum<LPR>(ss);
-    const float r = __builtin_amdgcn_rsqf(__fadd_rn(__fdiv_rn(ss, (float)D), eps));
+    const float r = norm_rsqrt<T>(__fadd_rn(__fdiv_rn(ss, (float)D), eps));
     const int half = D >> 1;
     const bool on = li * HV < half;
 #pragma unroll
@@ -262,7 +272,7 @@ struct Prologue {
 #pragma unroll
     for (int i = 0; i < VEC; ++i) ss = __builtin_fmaf(x[i], x[i], ss);
     ss = row_sum<LPR>(ss);
-    return __builtin_amdgcn_rsqf(__fadd_rn(__fdiv_rn(ss, (float)D), eps));
+    return norm_rsqrt<T>(__fadd_rn(__fdiv_rn(ss, (float)D), eps));
   }
 
   // forward() with the weights already in registers.

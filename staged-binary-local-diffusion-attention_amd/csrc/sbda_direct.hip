@@ -180,7 +180,7 @@ __global__ __launch_bounds__(kBlock) void bwd_dq_direct(Params p) {
 #pragma unroll
     for (int e = 0; e < VEC; ++e) ss = __builtin_fmaf(x[e], x[e], ss);
     ss = row_sum<LPR>(ss);
-    const float r = __builtin_amdgcn_rsqf(__fadd_rn(__fdiv_rn(ss, (float)p.D), p.eps));
+    const float r = norm_rsqrt<T>(__fadd_rn(__fdiv_rn(ss, (float)p.D), p.eps));
 #pragma unroll
     for (int e = 0; e < VEC; ++e) dw[e] = 0.f;
     PL::backward(dq, x, r, p.wq, c, s, li, p.D, dw);
@@ -248,7 +248,7 @@ __global__ __launch_bounds__(kBlock) void bwd_dkv_direct(Params p) {
 #pragma unroll
     for (int e = 0; e < VEC; ++e) ss = __builtin_fmaf(x[e], x[e], ss);
     ss = row_sum<LPR>(ss);
-    const float r = __builtin_amdgcn_rsqf(__fadd_rn(__fdiv_rn(ss, (float)p.D), p.eps));
+    const float r = norm_rsqrt<T>(__fadd_rn(__fdiv_rn(ss, (float)p.D), p.eps));
 #pragma unroll
     for (int e = 0; e < VEC; ++e) dw[e] = 0.f;
     PL::backward(dk, x, r, p.wk, c, s, li, p.D, dw);

@@ -436,14 +436,25 @@ def rope_tables(length: int, head_dim: int, theta: float,
                 device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
     """Device fp32 ``[length, head_dim/2]`` cos/sin tables (cached).
 
-    Kept in fp32 for every activation dtype: the reference evaluates the
-    angles and their cos/sin in fp32 (``attention_common.py:18-21``)."""
+    The angles and their cos/sin are evaluated in fp32 as the reference does
+    (``attention_common.py:16-19``); the reference then rounds the tables to
+    the activation dtype (``:20-21``), these stay fp32 for every dtype (a
+    deliberate difference: the parity bar is an fp32 reference).
+
+    A table is built outside HIP-graph capture only: built during capture, its
+    memory would come from the graph's pool and its fill kernel would run only
+    on replay, so eager calls before the first replay would read garbage.
+    Call once (a warm-up step) before capturing."""
     device = torch.device(device)
     key = (device, int(length), int(head_dim), float(theta))
     hit = _ROPE_CACHE.get(key)
     if hit is not None:
         _ROPE_CACHE.move_to_end(key)
         return hit
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError(
+            f"RoPE tables for length {length}, head_dim {head_dim}, theta {theta} are not "
+            "built yet; run one eager call (a warm-up step) before HIP-graph capture")
     inv = rope_inverse_frequencies(head_dim, theta).contiguous()
     cos = torch.empty((length, head_dim // 2), dtype=torch.float32, device=device)
     sin = torch.empty_like(cos)

@@ -18,6 +18,7 @@ import pytest
 import torch
 
 from oracle import sbda_oracle as ref
+from tests.sampled import sampled_oracle
 
 KATS = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())
 
@@ -247,6 +248,51 @@ def test_rope_frequencies_and_invariants():
     assert torch.equal(ref.apply_rope(xo, theta), xo)
 
 
+# RoFormer's rotation (Su et al. 2021, eq. 34, half-split pairing): the pair
+# (x[d], x[d + D/2]) at position m is multiplied by R(m * theta_d) =
+# [[cos, -sin], [sin, cos]].  D = 4, theta = 100: theta_0 = 1, theta_1 = 0.1.
+# cos/sin of the angles 1, 3, 0.1, 0.3 written out (not recomputed here).
+_C1, _S1 = 0.5403023058681398, 0.8414709848078965
+_C3, _S3 = -0.9899924966004454, 0.1411200080598672
+_C01, _S01 = 0.9950041652780258, 0.09983341664682815
+_C03, _S03 = 0.955336489125606, 0.29552020666133955
+ROPE_KAT = {
+    # (position, one-hot coordinate): expected output row
+    (1, 0): [_C1, 0.0, _S1, 0.0],
+    (1, 2): [-_S1, 0.0, _C1, 0.0],
+    (3, 0): [_C3, 0.0, _S3, 0.0],
+    (3, 2): [-_S3, 0.0, _C3, 0.0],
+    (1, 1): [0.0, _C01, 0.0, _S01],
+    (1, 3): [0.0, -_S01, 0.0, _C01],
+    (3, 1): [0.0, _C03, 0.0, _S03],
+    (3, 3): [0.0, -_S03, 0.0, _C03],
+}
+
+
+def _rope_kat_holds() -> bool:
+    theta = 100.0
+    for (m, coord), want in ROPE_KAT.items():
+        x = torch.zeros(1, 4, 1, 4, dtype=torch.float64)
+        x[0, :, 0, coord] = 1.0                      # the same one-hot at every position
+        y = ref.apply_rope(x, theta)[0, m, 0]
+        # fp32 angles and cos/sin (the reference's tables): agree to ~1e-7.
+        if not torch.allclose(y, torch.tensor(want, dtype=torch.float64), rtol=0, atol=1e-6):
+            return False
+    return True
+
+
+def test_rope_rotation_direction_known_answer():
+    assert ref.rope_inverse_frequencies(4, 100.0).tolist() == [1.0, 0.10000000149011612]
+    assert _rope_kat_holds()
+    # Rows at explicit positions (the sampled-row checks) are the same rows
+    # of the whole-sequence rotation, bit for bit.
+    x = _rand(2, 50, 3, 8, seed=34, dtype=torch.float32)
+    idx = torch.tensor([0, 3, 17, 49, 4])
+    full = ref.apply_rope(x, 10000.0)
+    torch.testing.assert_close(ref.apply_rope(x[:, idx], 10000.0, positions=idx), full[:, idx],
+                               rtol=0, atol=0)
+
+
 def test_prologue_gradcheck_fp64():
     theta = 10000.0
     q = _rand(1, 6, 2, 4, seed=30).requires_grad_()
@@ -288,6 +334,25 @@ def test_planted_mistakes_are_caught():
     # A dropped softmax scale or a transposed (k <-> v) operand also differs.
     assert not torch.allclose(ref.gather_attention(q * 8, k, v, offs), want, atol=1e-6)
     assert not torch.allclose(ref.gather_attention(q, v, k, offs), want, atol=1e-6)
+
+    # RoPE turned the other way (rotate_half as cat(x2, -x1): a rotation by
+    # -m*theta) keeps every invariant of test_rope_frequencies_and_invariants
+    # but fails the known answer.
+    orig_rot = ref.rotate_half
+
+    def flipped(x):
+        half = x.shape[-1] // 2
+        return torch.cat((x[..., half:], -x[..., :half]), dim=-1)
+
+    try:
+        ref.rotate_half = flipped
+        assert not _rope_kat_holds()
+        x = _rand(1, 40, 2, 8, seed=26)
+        y = ref.apply_rope(x, 10000.0)
+        torch.testing.assert_close(y[:, 0], x[:, 0], rtol=0, atol=0)   # still the identity at 0
+    finally:
+        ref.rotate_half = orig_rot
+    assert _rope_kat_holds()
 
 
 # ----------------------------------------------------------------- masks
@@ -422,3 +487,41 @@ def test_tables_gradcheck_fp64():
     idx, valid = _random_tables(b, t, s, seed=98)
     assert torch.autograd.gradcheck(
         lambda a, bb, c: ref.gather_attention_tables(a, bb, c, idx, valid), (q, k, v))
+
+
+# ------------------------------------------------ sampled-row helper
+
+@pytest.mark.parametrize("offs", [(0, 1), (0, 2), (0, 1, 2, 4), (0, 1, 2, 32), (0, 1, 2, 64)])
+@pytest.mark.parametrize("prologue", [False, True])
+def test_sampled_oracle_equals_whole_sequence_oracle(offs, prologue):
+    """The sampled-row evaluation used by the metric-size GPU tests gives the
+    whole-sequence oracle's rows (forward, and autograd's gradients, also
+    through the norm + RoPE prologue)."""
+    b, t, h, d = 1, 70, 3, 8
+    theta = 10000.0
+    q, k, v, g = (_rand(b, t, h, d, seed=60 + i, dtype=torch.float32) for i in range(4))
+    wq = 1 + 0.1 * _rand(d, seed=64, dtype=torch.float32)
+    wk = 1 + 0.1 * _rand(d, seed=65, dtype=torch.float32)
+    rq, rk, rv = (x.clone().requires_grad_() for x in (q, k, v))
+    qq, kk = ref.prologue(rq, rk, wq, wk, theta) if prologue else (rq, rk)
+    out = ref.gather_attention(qq.permute(0, 2, 1, 3), kk.permute(0, 2, 1, 3),
+                               rv.permute(0, 2, 1, 3), offs)
+    out.backward(g.permute(0, 2, 1, 3))
+    rows = torch.tensor([0, 1, 2, 5, 31, 32, 33, 40, 68, 69])
+
+    def fetch(pos):
+        a, c = q[0, pos], k[0, pos]
+        if prologue:
+            a, c = ref.prologue(a[None], c[None], wq, wk, theta, positions=pos)
+            a, c = a[0], c[0]
+        return a, c, v[0, pos], g[0, pos]
+
+    o_w, dq_w, dk_w, dv_w = sampled_oracle(fetch, offs, rows, t, d)
+    if prologue:
+        a, c = q[0, rows].clone().requires_grad_(), k[0, rows].clone().requires_grad_()
+        aa, cc = ref.prologue(a[None], c[None], wq, wk, theta, positions=rows)
+        dq_w, dk_w = torch.autograd.grad((aa[0], cc[0]), (a, c), (dq_w, dk_w))
+    want = (out.detach()[0].permute(1, 0, 2)[rows], rq.grad[0, rows], rk.grad[0, rows],
+            rv.grad[0, rows])
+    for got, w in zip((o_w, dq_w, dk_w, dv_w), want):
+        torch.testing.assert_close(got, w, rtol=1e-5, atol=1e-6)

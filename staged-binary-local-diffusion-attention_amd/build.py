@@ -2,7 +2,8 @@
 
 Each ``.hip`` file is compiled to an object with ``hipcc`` (in parallel),
 then linked into one shared library next to this file.  The library is
-rebuilt when forced or when a source or header is newer than it.
+rebuilt when forced (every source recompiled) or when a source or header is
+newer than it (only the stale objects recompiled).
 """
 
 from __future__ import annotations
@@ -53,8 +54,23 @@ def _stale() -> bool:
     return any(p.stat().st_mtime > stamp for p in deps)
 
 
+def _object(src: Path) -> Path:
+    return OBJDIR / (src.stem + ".o")
+
+
+def _object_stale(src: Path) -> bool:
+    """An object is rebuilt when it is missing or older than its source, a
+    header or this script (headers are shared, so any header change counts)."""
+    obj = _object(src)
+    if not obj.exists():
+        return True
+    stamp = obj.stat().st_mtime
+    deps = [src, Path(__file__), *CSRC.glob("*.h"), *INCLUDE.glob("*.h")]
+    return any(p.stat().st_mtime > stamp for p in deps)
+
+
 def _compile(src: Path, hipcc: str) -> Path:
-    obj = OBJDIR / (src.stem + ".o")
+    obj = _object(src)
     cmd = [hipcc, *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     err = "\n".join(l for l in res.stderr.splitlines()
@@ -72,9 +88,11 @@ def build_library(force: bool = False, verbose: bool = False) -> Path:
     hipcc = _hipcc()
     OBJDIR.mkdir(exist_ok=True)
     srcs = sources()
-    jobs = min(len(srcs), int(os.environ.get("MAX_JOBS", "8")) or 1)
+    todo = srcs if force else [s for s in srcs if _object_stale(s)]
+    jobs = max(1, min(len(todo), int(os.environ.get("MAX_JOBS", "8")) or 1))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(s, hipcc), srcs))
+        list(ex.map(lambda s: _compile(s, hipcc), todo))
+    objs = [_object(s) for s in srcs]
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)

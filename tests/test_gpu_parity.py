@@ -100,6 +100,16 @@ def test_bf16_fwd_bwd_layers(layer):
     _close(_fused(q, k, v, offs, g), _oracle(q, k, v, offs, g), LOW_TOL, f"bf16 layer {layer}")
 
 
+@pytest.mark.parametrize("layer", [1, 2])
+def test_far_free_full_tiles_at_t_2_17(layer):
+    # B = 1, T = 2^17: enough tiles that the far-free walks keep their full
+    # tile sizes (64-position forward tiles, 32-position backward tiles, as
+    # at the metric shape), checked in full against the oracle.
+    q, k, v, g = _inputs(1, 1 << 17, 8, 64, torch.bfloat16, seed=320 + layer)
+    offs = ref.sbda_layer_offsets(layer)
+    _close(_fused(q, k, v, offs, g), _oracle(q, k, v, offs, g), LOW_TOL, f"T=2^17 layer {layer}")
+
+
 def test_fp16_fwd_bwd():
     q, k, v, g = _inputs(1, 1000, 8, 64, torch.float16, seed=17)
     offs = (0, 1, 2, 16)

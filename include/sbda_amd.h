@@ -190,6 +190,34 @@ int sbda_backward_prologue(const void* q_raw, const int64_t* q_strides,
                            const int32_t* seg_key, void* stream);
 
 /*
+ * sbda_backward_prologue without a workspace argument: for callers that
+ * cannot allocate device memory (code under HIP-graph capture, tight serving
+ * or training loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  The workspace comes from a static device array of the library
+ * (sbda_noalloc_scratch_bytes() = 128 MiB, one copy per GPU, held until the
+ * process ends); calls needing more (sbda_backward_workspace_for) fail with
+ * SBDA_ERR_VALUE before launching anything.  Nothing is allocated.  Call it
+ * with the tensors' device current.  Calls that overlap on one GPU share the
+ * scratch and race; the scratch keeps the last call's contents.
+ */
+int64_t sbda_noalloc_scratch_bytes(void);
+int sbda_backward_prologue_noalloc(const void* q_raw, const int64_t* q_strides,
+                                   const void* k_raw, const int64_t* k_strides,
+                                   const void* v, const int64_t* v_strides,
+                                   const void* dout, const int64_t* dout_strides,
+                                   const float* lse,
+                                   const float* q_weight, const float* k_weight,
+                                   const float* rope_cos, const float* rope_sin, float eps,
+                                   void* dq_raw, const int64_t* dq_strides,
+                                   void* dk_raw, const int64_t* dk_strides,
+                                   void* dv, const int64_t* dv_strides,
+                                   float* dq_weight, float* dk_weight,
+                                   int64_t batch, int64_t heads, int64_t kv_heads,
+                                   int64_t length, int64_t head_dim, int32_t dtype,
+                                   const int32_t* offsets, int32_t num_offsets,
+                                   const int32_t* seg_key, void* stream);
+
+/*
  * Forward over source tables (see "Source tables" above).  Writes out and
  * lse like sbda_forward / sbda_forward_prologue.
  */

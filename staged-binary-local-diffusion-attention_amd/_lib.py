@@ -11,7 +11,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("libsbda_amd.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 OK, ERR_VALUE, ERR_DTYPE, ERR_RUNTIME = 0, 1, 2, 3
 _ERRORS = {ERR_VALUE: ValueError, ERR_DTYPE: TypeError, ERR_RUNTIME: RuntimeError}
@@ -46,6 +46,11 @@ SIGNATURES = {
                                               _strides, _fptr, _fptr, _fptr, _p, _p, _f32,
                                               _p, _strides, _p, _strides, _p, _strides,
                                               _fptr, _fptr, _p, _i64, *_SHAPE, _SEG, _p]),
+    "sbda_noalloc_scratch_bytes": (ctypes.c_int64, []),
+    "sbda_backward_prologue_noalloc": (ctypes.c_int, [_p, _strides, _p, _strides, _p, _strides,
+                                                      _p, _strides, _fptr, _fptr, _fptr, _p, _p,
+                                                      _f32, _p, _strides, _p, _strides, _p,
+                                                      _strides, _fptr, _fptr, *_SHAPE, _SEG, _p]),
     "sbda_forward_paths": (ctypes.c_int, [_p, _strides, _p, _strides, _p, _strides, _p, _strides,
                                           _fptr, _fptr, _fptr, _p, _p, _f32,
                                           _i64, _i64, _i64, _i64, _i64, _i32, _p, _p, _i32,

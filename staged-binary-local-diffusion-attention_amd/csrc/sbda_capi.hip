@@ -4,6 +4,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "sbda_amd.h"
@@ -366,6 +367,44 @@ int check_rows(int64_t rows, int64_t width, int32_t dtype, int64_t max_width) {
   return SBDA_OK;
 }
 
+// ------------------------------------------------ allocation-free backward
+//
+// sbda_backward_prologue_noalloc takes its workspace (norm-weight partial
+// rows, deferred chain slots, weight tables) from `scratch`, a fixed device
+// array of the library, instead of a caller allocation.  Every GPU the
+// library runs on holds its own copy until the process ends.  The host never
+// uses the array's name as an address: each device's address comes from
+// hipGetSymbolAddress, once per device, on the first call there.  No part of
+// the scratch has to start at zero: every partial row, slot and table entry
+// the kernels read is written earlier in the same call.  Calls that overlap
+// on one GPU (two streams, two threads) share the array and race.
+constexpr int64_t kScratchBytes = int64_t(128) << 20;
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's address of `scratch` (the caller's current device).
+int device_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(SBDA_ERR_RUNTIME, "device ordinal %d outside the scratch table", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e, "hipGetSymbolAddress(scratch)");
+    if (ptr == nullptr) return fail(SBDA_ERR_RUNTIME, "scratch has no address on device %d", dev);
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return SBDA_OK;
+}
+
 }  // namespace
 }  // namespace sbda
 
@@ -373,7 +412,7 @@ using namespace sbda;
 
 extern "C" {
 
-int sbda_abi_version(void) { return 9; }
+int sbda_abi_version(void) { return 10; }
 
 const char* sbda_last_error(void) { return g_error.c_str(); }
 
@@ -474,6 +513,37 @@ int sbda_backward_prologue(const void* q, const int64_t* qs, const void* k, cons
   return backward_impl(true, q, qs, k, ks, v, vs, dout, dos, lse, wq, wk, rc, rs, eps, dq, dqs, dk,
                        dks, dv, dvs, dwq, dwk, ws, ws_bytes, batch, heads, kv_heads, length, head_dim,
                        dtype, offsets, n, seg_key, stream);
+}
+
+int64_t sbda_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+int sbda_backward_prologue_noalloc(const void* q, const int64_t* qs, const void* k,
+                                   const int64_t* ks, const void* v, const int64_t* vs,
+                                   const void* dout, const int64_t* dos, const float* lse,
+                                   const float* wq, const float* wk, const float* rc,
+                                   const float* rs, float eps, void* dq, const int64_t* dqs,
+                                   void* dk, const int64_t* dks, void* dv, const int64_t* dvs,
+                                   float* dwq, float* dwk, int64_t batch, int64_t heads,
+                                   int64_t kv_heads, int64_t length, int64_t head_dim,
+                                   int32_t dtype, const int32_t* offsets, int32_t n,
+                                   const int32_t* seg_key, void* stream) {
+  // The exact need for these strides (the strides pick the kernel family);
+  // refused before anything is launched when the scratch cannot hold it.
+  const int64_t need = sbda_backward_workspace_for(1, qs, ks, vs, dos, dqs, dks, dvs, batch, heads,
+                                                   kv_heads, length, head_dim, dtype, offsets, n,
+                                                   seg_key);
+  if (need < 0) return (int)-need;
+  if (need > kScratchBytes)
+    return fail(SBDA_ERR_VALUE,
+                "allocation-free backward: this call needs %lld bytes of workspace, the library's "
+                "static scratch holds %lld; call sbda_backward_prologue with a workspace instead",
+                (long long)need, (long long)kScratchBytes);
+  void* ws = nullptr;
+  int rc_ = device_scratch(&ws);
+  if (rc_) return rc_;
+  return backward_impl(true, q, qs, k, ks, v, vs, dout, dos, lse, wq, wk, rc, rs, eps, dq, dqs, dk,
+                       dks, dv, dvs, dwq, dwk, ws, kScratchBytes, batch, heads, kv_heads, length,
+                       head_dim, dtype, offsets, n, seg_key, stream);
 }
 
 int sbda_forward_paths(const void* q, const int64_t* qs, const void* k, const int64_t* ks,

@@ -88,11 +88,26 @@ struct ChainCfg {
   int HG, nwg;
 };
 
-// W = 8 rows (fewer when the sequence has fewer rows), at most 4 when rows
-// are 32 MiB or more apart: eight lockstep waves on addresses that far apart
-// collide in the DRAM channel mapping.  One chain per workgroup (L = W):
-// shorter chains on more bands measured slower.
-inline ChainCfg make_chain_cfg(int64_t B, int64_t row_stride_bytes, const WalkCfg& wc) {
+// Row pairs (the plain backward): a workgroup of 8 waves holds chains of 2
+// rows on 4 adjacent bands, row blocks fastest, so a workgroup's waves sit on
+// 2 rows of 4 consecutive tiles and the rows beyond the pair (the first
+// row's far-left sources, the second row's far queries) are the own rows of
+// the workgroups beside it, fetched at about the same time on the same XCD.
+// Measured at T = 2^20 against 8-row chains on 128-position tiles: layers
+// 9-11 and 15-20 1.49-1.58 -> 1.34-1.47 ms.  Not at row strides of 4-8 MiB,
+// where pairs of rows collide in the DRAM channel mapping (layer 13: 1.54 ->
+// 1.72 ms); those keep the 8-row chains.
+inline bool chain_pairs_apply(const WalkCfg& wc, int64_t row_stride_bytes) {
+  const int64_t fs = (int64_t)wc.F * row_stride_bytes;
+  return wc.F >= 128 && wc.rows >= 2 && !(fs >= ((int64_t)4 << 20) && fs <= ((int64_t)8 << 20));
+}
+
+// Otherwise W = 8 rows (fewer when the sequence has fewer rows), at most 4
+// when rows are 32 MiB or more apart: eight lockstep waves on addresses that
+// far apart collide in the DRAM channel mapping.  One chain per workgroup
+// (L = W).
+inline ChainCfg make_chain_cfg(int64_t B, int64_t row_stride_bytes, const WalkCfg& wc,
+                               bool pairs = false) {
   ChainCfg c{};
   c.P = wc.P;
   c.F = wc.F;
@@ -100,6 +115,10 @@ inline ChainCfg make_chain_cfg(int64_t B, int64_t row_stride_bytes, const WalkCf
   c.W = c.rows >= 8 ? 8 : c.rows >= 4 ? 4 : c.rows >= 2 ? 2 : 1;
   if ((int64_t)wc.F * row_stride_bytes >= kBigStride && c.W > 4) c.W = 4;
   c.L = c.W;
+  if (pairs) {
+    c.W = kPipeWaves;
+    c.L = 2;
+  }
   c.bands = wc.F / wc.P;
   c.blocks = (c.rows + c.L - 1) / c.L;
   c.bgroups = (c.bands + c.W / c.L - 1) / (c.W / c.L);
@@ -259,7 +278,9 @@ struct Raw {
 // re-reads them in the kernel).  A row a wave loads for its own position is
 // re-read by no other wave when the pattern has no far offset, so those loads
 // are non-temporal too; with a far offset the neighbouring wave (column t + F)
-// reads the same rows, and they must stay in L2 / the Infinity Cache.
+// reads the same k/v rows, and they must stay in L2 / the Infinity Cache.
+// The forward's q rows are read by their own position only: non-temporal in
+// every pattern (far forwards at T = 2^20: 0.42 ms less per 20-layer step).
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <typename T>

@@ -118,7 +118,16 @@ WalkCfg launch_cfg(const Params& p, int dtype, const Pattern& pat, int lpr, bool
   // Not the backward (4 halo rows; 64-position tiles measured 2-7% slower)
   // nor the forward with far offsets 4 and 8 (6-7% slower).
   const int lin = (fwd && !pro && pat.far == 0) ? 64 : 32;
-  WalkCfg c = make_pipe_cfg(p, lpr, pat, 128, lin);
+  // The plain backward's row-pair chains take 64-position tiles (32 at F =
+  // 128, so a workgroup still finds 4 bands); 32- and 128-position tiles
+  // measured slower at F >= 256.
+  int col_tile = 128;
+  if (!fwd && !pro && pat.far >= 128) {
+    WalkCfg probe = make_pipe_cfg(p, lpr, pat, 64, lin);
+    if (probe.column && walk::chain_pairs_apply(probe, far_stride_bytes(p, pat, dtype) / pat.far))
+      col_tile = pat.far >= 256 ? 64 : 32;
+  }
+  WalkCfg c = make_pipe_cfg(p, lpr, pat, col_tile, lin);
   if ((fwd || pro) && c.column && c.rows > 4 && far_stride_bytes(p, pat, dtype) >= kBigStride) {
     c.rg = 4;
     order_tiles(p, pat, (int64_t)p.B * c.HG, c);

@@ -764,7 +764,8 @@ __global__ __launch_bounds__(64 * F) void bwd_tc(Params p, TcCfg cfg) {
 
 template <typename T, int LPR, int NM>
 hipError_t launch_chain(const Params& p, const WalkCfg& wc, hipStream_t st) {
-  const ChainCfg c = make_chain_cfg(p.B, p.q.st * (int64_t)sizeof(T), wc);
+  const int64_t stride = p.q.st * (int64_t)sizeof(T);
+  const ChainCfg c = make_chain_cfg(p.B, stride, wc, chain_pairs_apply(wc, stride));
   if (c.nwg <= 0) return hipErrorInvalidValue;
   const dim3 grid((unsigned)c.nwg), block(64 * c.W);
   switch (c.W) {

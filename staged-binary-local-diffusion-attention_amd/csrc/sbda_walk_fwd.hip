@@ -49,7 +49,7 @@ struct FwdPipe {
       vraw[R & 1] = load_at<!FAR>(v, tc);
     }
     if (q_ok) {
-      qn[R & 1] = load_at<!FAR>(q, tc);
+      qn[R & 1] = load_at<true>(q, tc);
       if constexpr (FAR && FR == 0) {
         const int tf = clampi(t - F, Tm1);
         kl[R & 1] = load_at(k, tf);

@@ -110,6 +110,16 @@ def test_far_free_full_tiles_at_t_2_17(layer):
     _close(_fused(q, k, v, offs, g), _oracle(q, k, v, offs, g), LOW_TOL, f"T=2^17 layer {layer}")
 
 
+@pytest.mark.parametrize("b,t,h,offs", [(2, 40000, 16, (0, 1, 2, 16384)), (1, 70000, 8, (0, 32768)),
+                                         (3, 16385, 8, (0, 1, 2, 16384))])
+def test_column_strip_walks(b, t, h, offs):
+    # Far offsets >= 16384 walk column strips (a workgroup on 8 consecutive
+    # tiles of one row, rows fastest): partial last rows, several head groups
+    # and batches, far-only patterns, a last row of one position.
+    q, k, v, g = _inputs(b, t, h, 64, torch.bfloat16, seed=t + h + offs[-1])
+    _close(_fused(q, k, v, offs, g), _oracle(q, k, v, offs, g), LOW_TOL, f"strips B={b} T={t} {offs}")
+
+
 def test_fp16_fwd_bwd():
     q, k, v, g = _inputs(1, 1000, 8, 64, torch.float16, seed=17)
     offs = (0, 1, 2, 16)

@@ -25,6 +25,7 @@ import torch
 from torch import Tensor, nn
 from torch.nn import functional as F
 
+from ._weights import StackedRows
 from .sbda import fused_sbda_prologue, segment_keys
 from .topology import PATH_TOPOLOGIES, topology_offsets
 
@@ -77,6 +78,8 @@ class BinaryPathAttention(nn.Module):
         self.q_norm = _HeadRMSNorm(self.head_dim)
         self.k_norm = _HeadRMSNorm(self.head_dim)
         self.out = nn.Linear(dim, dim, bias=False)
+        # [q; k; v] rows for the one projection GEMM, rebuilt only when a weight changes.
+        self._qkv_weight = StackedRows()
 
     def _check_inputs(self, x, valid_mask, seam_reset, path_indices, path_valid):
         # Same validation and messages as left_v2.py:199-232.
@@ -133,7 +136,7 @@ class BinaryPathAttention(nn.Module):
         # One GEMM for q, k and v; the kernels read the three column blocks of
         # its output in place (strided views, no copies).
         kvd = self.kv_heads * self.head_dim
-        qkv = F.linear(x, torch.cat((self.q.weight, self.k.weight, self.v.weight), dim=0))
+        qkv = F.linear(x, self._qkv_weight(self.q.weight, self.k.weight, self.v.weight))
         q = qkv[..., :dim].view(batch, length, self.heads, self.head_dim)
         k = qkv[..., dim:dim + kvd].view(batch, length, self.kv_heads, self.head_dim)
         v = qkv[..., dim + kvd:].view(batch, length, self.kv_heads, self.head_dim)

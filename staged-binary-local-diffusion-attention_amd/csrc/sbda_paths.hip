@@ -13,7 +13,8 @@
 // log-normaliser per row.  Backward, deterministic and atomic-free:
 //   1. `path_keys`: each (b, i, s) entry gets the key b*T + j (or B*T when it
 //      does not count) and the value i*S + s;
-//   2. a stable radix sort (hipCUB) orders entries by key, ties by (i, s);
+//   2. a stable LSD radix sort (rocPRIM, only the bits of the largest key)
+//      orders entries by key, ties keep their (i, s) order;
 //   3. `path_starts`: per key, the first sorted entry (binary search);
 //   4. `bwd_q_paths`: dQ per query row, and per (row, slot) the pair
 //      (p, scale * dS) into a table;
@@ -21,7 +22,7 @@
 //      queries that read it, in sorted (i, s) order.
 
 #include <hip/hip_runtime.h>
-#include <hipcub/device/device_radix_sort.hpp>
+#include <rocprim/device/device_radix_sort.hpp>
 
 #include "sbda_rows.h"
 
@@ -281,10 +282,9 @@ int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
 int64_t sort_temp_bytes(int64_t n, int64_t max_key) {
   size_t bytes = 0;
-  if (hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, (const uint32_t*)nullptr,
-                                         (uint32_t*)nullptr, (const uint32_t*)nullptr,
-                                         (uint32_t*)nullptr, (int)n, 0, end_bit(max_key),
-                                         (hipStream_t)0) != hipSuccess)
+  if (rocprim::radix_sort_pairs(nullptr, bytes, (const uint32_t*)nullptr, (uint32_t*)nullptr,
+                                (const uint32_t*)nullptr, (uint32_t*)nullptr, (size_t)n, 0,
+                                (unsigned)end_bit(max_key), (hipStream_t)0) != hipSuccess)
     return -1;
   return (int64_t)bytes;
 }
@@ -385,8 +385,9 @@ hipError_t paths_backward(Params p, int dtype, bool pro, void* ws, int64_t parts
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   size_t tb = (size_t)temp;
-  e = hipcub::DeviceRadixSort::SortPairs(sort_tmp, tb, keys_in, keys_out, vals_in, vals_out, (int)n,
-                                         0, end_bit(bt), st);
+  e = rocprim::radix_sort_pairs(sort_tmp, tb, (const uint32_t*)keys_in, keys_out,
+                                (const uint32_t*)vals_in, vals_out, (size_t)n, 0,
+                                (unsigned)end_bit(bt), st);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(path_starts, dim3((unsigned)((bt + 1 + kBlock - 1) / kBlock)), dim3(kBlock), 0,
                      st, keys_out, n, bt, starts);

@@ -749,7 +749,15 @@ __device__ inline void get_rows(const float4 (&src)[VEC / 4][64], int lane, floa
   }
 }
 
-template <typename T, int LPR, int NM, bool LEFT_LDS, bool RIGHT_LDS>
+// RoPE cos/sin of the last 4 positions a wave walked, in LDS: [u & 3][lane
+// in row][cos (HV), sin (HV)].  A position's entries are loaded with the rows
+// one step ahead and stashed here once they arrive, so no table load sits
+// inside a step: such a load (its result needed at once) made every step wait
+// for the next step's row loads too, serialising load latency and VALU work.
+template <int LPR, int HV>
+using CsRing = float[4][LPR][2 * HV];
+
+template <typename T, int LPR, int NM, bool LEFT_LDS, bool RIGHT_LDS, bool RING>
 struct BwdChainPro : ProBase<T, LPR> {
   using B_ = ProBase<T, LPR>;
   using B_::VEC;
@@ -773,8 +781,10 @@ struct BwdChainPro : ProBase<T, LPR> {
   float lr[2];
   Raw kl[2], vl[2];            // far-left raw rows of query u (first wave)
   float clc[2][HV], cls[2][HV];
+  float cpf[HV], spf[HV];      // cos/sin of the position in flight (RING)
+  float (*ring)[LPR][2 * HV];  // this wave's CsRing (RING)
   float kh[4][VEC];            // roped k rotation
-  float qh[4][VEC];            // roped q rotation
+  float qh[VEC];               // roped q of this step (earlier steps' rows: mine->qf)
   float rk[4];
   float sp[4][3], sd[4][3];
   float dwq[VEC], dwk[VEC];
@@ -793,6 +803,42 @@ struct BwdChainPro : ProBase<T, LPR> {
       vl[R & 1] = load_split(v, ul);
       this->cs(ul, clc[R & 1], cls[R & 1]);
     }
+    if constexpr (RING) this->cs(uc, cpf, spf);
+  }
+
+  // The arrived cos/sin of step R's position into the ring (before the next
+  // prefetch reuses cpf/spf).  The first head's lanes write and every lane
+  // reads: a wavefront-scope fence orders those cross-lane LDS accesses (no
+  // wait is needed within one wave, but the compiler must not move the reads
+  // above the writes).
+  template <int R>
+  __device__ inline void stash() {
+    if constexpr (RING) {
+      if (hl == 0) {
+#pragma unroll
+        for (int i = 0; i < HV; ++i) {
+          ring[R][this->li][i] = cpf[i];
+          ring[R][this->li][HV + i] = spf[i];
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  }
+
+  // cos/sin of step R's position (u clamped into the sequence).
+  template <int R>
+  __device__ inline void cs_of(int u, float (&c)[HV], float (&s)[HV]) const {
+    if constexpr (RING) {
+#pragma unroll
+      for (int i = 0; i < HV; ++i) {
+        c[i] = ring[R][this->li][i];
+        s[i] = ring[R][this->li][HV + i];
+      }
+    } else {
+      this->cs(clampi(u, this->Tm1), c, s);
+    }
   }
 
   // dK' -> dK through the transposed prologue, then both rows out.
@@ -800,7 +846,7 @@ struct BwdChainPro : ProBase<T, LPR> {
   __device__ inline void finish_key(int j, float (&ak)[VEC], const float (&av)[VEC]) {
     float kx[VEC], cj[HV], sj[HV];
     widen<T>(kr[(R + 2) & 3], kx);
-    this->cs(clampi(j, this->Tm1), cj, sj);
+    cs_of<(R + 2) & 3>(j, cj, sj);
     PL::backward_w(ak, kx, rk[(R + 2) & 3], this->wk, cj, sj, this->D, dwk);
     store_split<T>(dk, j, ak);
     store_split<T>(dv, j, av);
@@ -809,17 +855,17 @@ struct BwdChainPro : ProBase<T, LPR> {
   template <int R>
   __device__ inline void compute(int u) {
     float cu[HV], su[HV];
-    this->cs(clampi(u, this->Tm1), cu, su);
+    cs_of<R>(u, cu, su);
     rk[R] = this->rope(kr[R], this->wk, cu, su, kh[R]);
     float qx[VEC];
     widen<T>(qr[R & 1], qx);
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) qh[R][e] = qx[e];
-    const float rq = PL::forward_w(qh[R], this->wq, cu, su, this->D, this->eps);
+    for (int e = 0; e < VEC; ++e) qh[e] = qx[e];
+    const float rq = PL::forward_w(qh, this->wq, cu, su, this->D, this->eps);
     // Publish this step's rows, then wait for the neighbours'.
     put_rows<VEC>(mine->kf[R & 1], lane, kh[R]);
     mine->vf[R & 1][lane] = pack_raw(vr[R]);
-    put_rows<VEC>(mine->qf[R], lane, qh[R]);
+    put_rows<VEC>(mine->qf[R], lane, qh);
     mine->gf[R][lane] = pack_raw(gr[R]);
     __syncthreads();
     float kfar[VEC];
@@ -853,7 +899,7 @@ struct BwdChainPro : ProBase<T, LPR> {
       for (int s_ = 0; s_ < NS; ++s_) {
         float a_ = 0.f;
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) a_ = __builtin_fmaf(qh[R][e], ks[s_][e], a_);
+        for (int e = 0; e < VEC; ++e) a_ = __builtin_fmaf(qh[e], ks[s_][e], a_);
         const float sc = row_sum<LPR>(a_) * scale;
         dp[s_] = row_sum<LPR>(dot_raw<T>(gr[R], *vs[s_]));
         pp[s_] = ok[s_] ? fast_exp(sc - lr[R & 1]) : 0.f;
@@ -900,11 +946,17 @@ struct BwdChainPro : ProBase<T, LPR> {
           const bool there = j + n < T_;
           const float cs_ = there ? sd[slot][idx] : 0.f;
           const float cp_ = there ? sp[slot][idx] : 0.f;
-          float gx[VEC];
+          float gx[VEC], qs[VEC];
           widen<T>(gr[slot], gx);
+          if (slot == R) {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) qs[e] = qh[e];
+          } else {
+            get_rows<VEC>(mine->qf[slot], lane, qs);   // this wave's own earlier row
+          }
 #pragma unroll
           for (int e = 0; e < VEC; ++e) {
-            ak[e] = __builtin_fmaf(cs_, qh[slot][e], ak[e]);
+            ak[e] = __builtin_fmaf(cs_, qs[e], ak[e]);
             av[e] = __builtin_fmaf(cp_, gx[e], av[e]);
           }
           ++idx;
@@ -947,26 +999,33 @@ struct BwdChainPro : ProBase<T, LPR> {
     // u = a-2 .. a+P+1 for every wave of the workgroup (same trip count).
     this->template prefetch<0>(u0);
     for (int u = u0; u <= end_u; u += 4) {
+      stash<0>();
       this->template prefetch<1>(u + 1);
       this->template compute<0>(u);
+      stash<1>();
       this->template prefetch<2>(u + 2);
       this->template compute<1>(u + 1);
+      stash<2>();
       this->template prefetch<3>(u + 3);
       this->template compute<2>(u + 2);
+      stash<3>();
       this->template prefetch<0>(u + 4);
       this->template compute<3>(u + 3);
     }
   }
 };
 
-template <typename T, int LPR, int NM, bool LEFT_LDS, bool RIGHT_LDS, int W>
+template <typename T, int LPR, int NM, bool LEFT_LDS, bool RIGHT_LDS, int W, bool RING>
 __device__ inline void chain_pro_wave(const Params& p, const ChainCfg& c,
-                                      ChainProSlot<VecOf<T>::value>* lds, int w, int b, int hg,
-                                      int rb, int cb, int a, float (&dw)[2][VecOf<T>::value]) {
+                                      ChainProSlot<VecOf<T>::value>* lds,
+                                      CsRing<LPR, VecOf<T>::value / 2>* rings, int w, int b,
+                                      int hg, int rb, int cb, int a,
+                                      float (&dw)[2][VecOf<T>::value]) {
   constexpr int VEC = VecOf<T>::value, esz = (int)sizeof(T);
   const int lane = threadIdx.x & 63, hl = lane / LPR, li = lane % LPR;
   const int h0 = hg * (64 / LPR);
-  BwdChainPro<T, LPR, NM, LEFT_LDS, RIGHT_LDS> x;
+  BwdChainPro<T, LPR, NM, LEFT_LDS, RIGHT_LDS, RING> x;
+  x.ring = rings[RING ? w : 0];
 #pragma unroll
   for (int e = 0; e < VEC; ++e) {
     x.dwq[e] = 0.f;
@@ -1012,7 +1071,13 @@ __device__ inline void chain_pro_wave(const Params& p, const ChainCfg& c,
 
 template <typename T, int LPR, int NM, int W>
 __global__ __launch_bounds__(64 * W) void bwd_chain_pro(Params p, ChainCfg c) {
-  __shared__ ChainProSlot<VecOf<T>::value> lds[W];
+  constexpr int VEC = VecOf<T>::value;
+  // The cos/sin rings where they fit beside the rows' rings in one CU's LDS
+  // (all but 16-lane rows of 16-bit types: head_dim 128).
+  constexpr bool RING =
+      sizeof(ChainProSlot<VEC>) * W + sizeof(CsRing<LPR, VEC / 2>) * W <= 160 * 1024;
+  __shared__ ChainProSlot<VEC> lds[W];
+  __shared__ CsRing<LPR, VEC / 2> rings[RING ? W : 1];
   const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   // Workgroup -> (batch, head group, band, row block), XCD-contiguous; wave w
   // -> row w of the block (one chain per workgroup).
@@ -1028,14 +1093,14 @@ __global__ __launch_bounds__(64 * W) void bwd_chain_pro(Params p, ChainCfg c) {
   const int a = (r < c.rows && a64 < p.T) ? (int)a64 : p.T;
   float dw[2][VecOf<T>::value];
   if constexpr (W == 1) {
-    chain_pro_wave<T, LPR, NM, false, false, W>(p, c, lds, w, b, hg, rb, cb, a, dw);
+    chain_pro_wave<T, LPR, NM, false, false, W, RING>(p, c, lds, rings, w, b, hg, rb, cb, a, dw);
   } else {
     if (w == 0)
-      chain_pro_wave<T, LPR, NM, false, true, W>(p, c, lds, w, b, hg, rb, cb, a, dw);
+      chain_pro_wave<T, LPR, NM, false, true, W, RING>(p, c, lds, rings, w, b, hg, rb, cb, a, dw);
     else if (w == W - 1)
-      chain_pro_wave<T, LPR, NM, true, false, W>(p, c, lds, w, b, hg, rb, cb, a, dw);
+      chain_pro_wave<T, LPR, NM, true, false, W, RING>(p, c, lds, rings, w, b, hg, rb, cb, a, dw);
     else
-      chain_pro_wave<T, LPR, NM, true, true, W>(p, c, lds, w, b, hg, rb, cb, a, dw);
+      chain_pro_wave<T, LPR, NM, true, true, W, RING>(p, c, lds, rings, w, b, hg, rb, cb, a, dw);
   }
   // One norm-weight partial row per workgroup (the rings' LDS is free now).
   float* const parts[2] = {p.dwq_part, p.dwk_part};

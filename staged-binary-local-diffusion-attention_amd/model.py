@@ -25,6 +25,7 @@ import torch
 from torch import Tensor, nn
 from torch.nn import functional as F
 
+from ._weights import StackedRows
 from .attention import SBDAttention
 from .block import (fused_add_rms_norm, fused_rms_norm, fused_swiglu, fused_swiglu_gemm,
                     swiglu_gemm_supported)
@@ -66,13 +67,16 @@ class SwiGLU(nn.Module):
         self.up = nn.Linear(dim, hidden, bias=bias)
         self.down = nn.Linear(hidden, dim, bias=bias)
         self.dropout = nn.Dropout(dropout)
+        # [gate; up] rows (and biases) for the one GEMM, rebuilt only when they change.
+        self._gate_up_weight = StackedRows()
+        self._gate_up_bias = StackedRows()
 
     def forward(self, x: Tensor) -> Tensor:
         if not x.is_cuda:
             return self.dropout(self.down(F.silu(self.gate(x)) * self.up(x)))
-        weight = torch.cat((self.gate.weight, self.up.weight), dim=0)
+        weight = self._gate_up_weight(self.gate.weight, self.up.weight)
         bias = (None if self.gate.bias is None
-                else torch.cat((self.gate.bias, self.up.bias), dim=0))
+                else self._gate_up_bias(self.gate.bias, self.up.bias))
         if not torch.is_grad_enabled() and swiglu_gemm_supported(x, weight):
             # No gradient needed: the [gate | up] GEMM with the activation in
             # its epilogue, one MFMA kernel.

@@ -236,3 +236,34 @@ def test_swiglu_gemm_validation_without_launching():
         sbda_amd.fused_swiglu_gemm(torch.zeros(4, 64, dtype=torch.bfloat16),
                                    torch.zeros(256, 64, dtype=torch.bfloat16))
     assert not sbda_amd.swiglu_gemm_supported(torch.zeros(4, 64), torch.zeros(256, 64))
+
+
+def test_stacked_rows_cache_matches_cat_and_its_gradient():
+    from sbda_amd._weights import StackedRows
+
+    g = torch.Generator().manual_seed(3)
+    a = torch.randn(4, 6, generator=g, requires_grad=True)
+    b = torch.randn(2, 6, generator=g, requires_grad=True)
+    rows = StackedRows()
+    x = torch.randn(5, 6, generator=g)
+    w = rows(a, b)
+    assert torch.equal(w, torch.cat((a, b)))
+    up = torch.randn(5, 6, generator=g)
+    (x @ w.T).mul(up[:, :6]).sum().backward()
+    ga, gb = a.grad.clone(), b.grad.clone()
+    a.grad = b.grad = None
+    (x @ torch.cat((a, b)).T).mul(up[:, :6]).sum().backward()
+    assert torch.allclose(ga, a.grad) and torch.allclose(gb, b.grad)
+    # Served from the cache until a parameter changes in place.
+    first = rows._buf
+    before = torch.cat((a, b)).detach().clone()
+    rows(a, b)
+    assert rows._buf is first
+    with torch.no_grad():
+        a.add_(1.0)
+    w2 = rows(a, b)
+    assert rows._buf is not first and torch.equal(w2, torch.cat((a, b)))
+    # The earlier output keeps its values (the cache is rebuilt, not overwritten).
+    assert torch.equal(w.detach(), before)
+    with torch.no_grad():
+        assert not rows(a, b).requires_grad

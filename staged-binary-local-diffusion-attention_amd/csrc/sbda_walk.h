@@ -354,6 +354,28 @@ __device__ inline void store_at(const Stream& s, int t, const float (&x)[VecOf<T
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(const_cast<char*>(s.base) + (uint64_t)s.at(t)));
 }
 
+// A row load that may be skipped, without a branch: a buffer load whose
+// offset lies past the resource's range returns zeros and touches no memory.
+// The load stays in the wave's in-order count of outstanding loads, so the
+// wait before the next use stays exact (a branch around a load made the
+// compiler wait for every load in flight, the next step's prefetch included).
+// Every walk span is below kSkipOffset (walk_applies).
+constexpr uint32_t kSkipOffset = 0xFFFFFF00u;
+
+template <bool NT = false>
+__device__ inline Raw load_at_if(const Stream& s, int t, bool ok) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(s.base), (short)0, kSkipOffset, 0x00020000);
+  const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, ok ? s.at(t) : kSkipOffset, 0, NT ? 2 : 0);
+  return Raw{{x.x, x.y, x.z, x.w}};
+}
+
+__device__ inline float load_f32_if(const Stream& s, int t, bool ok) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(s.base), (short)0, kSkipOffset, 0x00020000);
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, ok ? s.at(t) : kSkipOffset, 0, 0));
+}
+
 __device__ inline float load_f32(const Stream& s, int t) {
   return *reinterpret_cast<const float*>(s.base + (uint64_t)s.at(t));
 }

@@ -163,7 +163,7 @@ bool span_fits_32(const Vw& vw, const Params& p, int esz, int lpr) {
   if (vw.st < 0 || vw.sh < 0) return false;
   const int64_t span =
       ((int64_t)(p.T - 1) * vw.st + (int64_t)(64 / lpr - 1) * vw.sh) * esz + 16 * lpr;
-  return span <= (int64_t)0xffffffffLL;
+  return span <= (int64_t)walk::kSkipOffset;
 }
 
 bool walk_applies(const Params& p, int dtype) {

@@ -28,24 +28,29 @@ struct BwdPipe {
   float li_[2];
   float sp[4][3], sd[4][3];  // query u's near-slot p_n and scale * dS_n
 
+  // Rows of step u.  The two warm-up steps before the tile (u < a) only
+  // provide k and v (near sources of the first queries): their queries and
+  // far rows feed nothing that is stored, so those loads are skipped
+  // (load_at_if: zeros, no traffic).
   template <int R>
   __device__ inline void prefetch(int u) {
     const int uc = clampi(u, Tm1);
+    const bool live = u >= a;
     kr[R] = load_at<!FAR>(k, uc);
     vr[R] = load_at<!FAR>(v, uc);
-    qr[R] = load_at<!FAR>(q, uc);
-    gr[R] = load_at<!FAR>(go, uc);
-    lr[R] = load_f32(lse, uc);
+    qr[R] = load_at_if<!FAR>(q, uc, live);
+    gr[R] = load_at_if<!FAR>(go, uc, live);
+    lr[R] = load_f32_if(lse, uc, live);
     if constexpr (FAR) {
       const int ul = clampi(u - F, Tm1);
-      kl[R & 1] = load_at(k, ul);
-      vl[R & 1] = load_at(v, ul);
+      kl[R & 1] = load_at_if(k, ul, live);
+      vl[R & 1] = load_at_if(v, ul, live);
       const int i = clampi(u - 2 + F, Tm1);
-      fk[R] = load_at(k, i);
-      fv[R] = load_at(v, i);
-      qi[R & 1] = load_at(q, i);
-      gi[R & 1] = load_at(go, i);
-      li_[R & 1] = load_f32(lse, i);
+      fk[R] = load_at_if(k, i, live);
+      fv[R] = load_at_if(v, i, live);
+      qi[R & 1] = load_at_if(q, i, live);
+      gi[R & 1] = load_at_if(go, i, live);
+      li_[R & 1] = load_f32_if(lse, i, live);
     }
   }
 
@@ -257,26 +262,31 @@ struct BwdChain {
   float li_[2];
   float sp[4][3], sd[4][3];
 
+  // As BwdPipe::prefetch: the warm-up steps (u < a) load only k and v.
+  // Their q / dO rows are still published (zeros) and read by nobody who
+  // stores: wave w - 1 finishes its keys j from this wave's queries j + F,
+  // all of them at or after a.
   template <int R>
   __device__ inline void prefetch(int u) {
     const int uc = clampi(u, Tm1);
+    const bool live = u >= a;
     kr[R] = load_at(k, uc);
     vr[R] = load_at(v, uc);
-    qr[R] = load_at(q, uc);
-    gr[R] = load_at(go, uc);
-    lr[R] = load_f32(lse, uc);
+    qr[R] = load_at_if(q, uc, live);
+    gr[R] = load_at_if(go, uc, live);
+    lr[R] = load_f32_if(lse, uc, live);
     if constexpr (!LEFT_LDS) {
       const int ul = clampi(u - F, Tm1);
-      kl[R & 1] = load_at(k, ul);
-      vl[R & 1] = load_at(v, ul);
+      kl[R & 1] = load_at_if(k, ul, live);
+      vl[R & 1] = load_at_if(v, ul, live);
     }
     if constexpr (!RIGHT_LDS) {
       const int i = clampi(u - 2 + F, Tm1);
-      fk[R] = load_at(k, i);
-      fv[R] = load_at(v, i);
-      qi[R & 1] = load_at(q, i);
-      gi[R & 1] = load_at(go, i);
-      li_[R & 1] = load_f32(lse, i);
+      fk[R] = load_at_if(k, i, live);
+      fv[R] = load_at_if(v, i, live);
+      qi[R & 1] = load_at_if(q, i, live);
+      gi[R & 1] = load_at_if(go, i, live);
+      li_[R & 1] = load_f32_if(lse, i, live);
     }
   }
 

@@ -39,22 +39,18 @@ struct FwdPipe {
   // Rows of position t.  A query row (and its far source) only for positions
   // the tile stores (q_ok); k and v also for the warm-up positions before the
   // tile, whose rows are the first queries' sources, but not past its end
-  // (kv_ok).  Both flags are wave-uniform; a skipped row leaves its slot
-  // stale, and only steps that store nothing read such a slot.
+  // (kv_ok).  A skipped row reads zeros and moves no bytes (load_at_if); only
+  // steps that store nothing read such a slot.
   template <int R>
   __device__ inline void prefetch(int t, bool q_ok, bool kv_ok) {
     const int tc = clampi(t, Tm1);
-    if (kv_ok) {
-      kr[R] = load_at<!FAR>(k, tc);
-      vraw[R & 1] = load_at<!FAR>(v, tc);
-    }
-    if (q_ok) {
-      qn[R & 1] = load_at<true>(q, tc);
-      if constexpr (FAR && FR == 0) {
-        const int tf = clampi(t - F, Tm1);
-        kl[R & 1] = load_at(k, tf);
-        vl[R & 1] = load_at(v, tf);
-      }
+    kr[R] = load_at_if<!FAR>(k, tc, kv_ok);
+    vraw[R & 1] = load_at_if<!FAR>(v, tc, kv_ok);
+    qn[R & 1] = load_at_if<true>(q, tc, q_ok);
+    if constexpr (FAR && FR == 0) {
+      const int tf = clampi(t - F, Tm1);
+      kl[R & 1] = load_at_if(k, tf, q_ok);
+      vl[R & 1] = load_at_if(v, tf, q_ok);
     }
   }
 

@@ -98,13 +98,18 @@ WalkCfg launch_cfg(const Params& p, int dtype, const Pattern& pat, int lpr, bool
     // Measured at T = 2^20 over layers 8-20: 16.8 ms of forwards against
     // 17.3 ms with 8 rows x 128 positions per workgroup.
     // (Fewer than 4 bands: more rows per group, so no wave is left idle.)
-    // Rows 4-8 MiB apart are the exception: pairs of rows that far apart
-    // collide in the DRAM channel mapping, 8 rows x 1 band do not (layers 13
-    // and 14 at T = 2^20: 1.01 -> 0.89 ms and 0.91 -> 0.86 ms, two boxes).
-    WalkCfg c = make_pipe_cfg(p, lpr, pat, 64);
+    // Rows 4 MiB apart are the exception: pairs of 64-position rows that far
+    // apart collide in the DRAM channel mapping, 8 rows x 1 band do not
+    // (layer 13 at T = 2^20: 1.01 -> 0.89 ms, two boxes).  From 8 MiB up, with
+    // at least 4 rows, pairs of 32-position tiles (2 rows x 4 bands of 32)
+    // measured faster than 64 (layers 14-19: 0.76-0.80 against 0.75-0.87 ms,
+    // two boxes); not with 2 rows (layer 20: 0.80 against 0.74 ms).
+    const int64_t fs = far_stride_bytes(p, pat, dtype);
+    const int64_t rows = (p.T + pat.far - 1) / pat.far;
+    const bool narrow = fs >= ((int64_t)8 << 20) && rows >= 4;
+    WalkCfg c = make_pipe_cfg(p, lpr, pat, narrow ? 32 : 64);
     if (c.column && c.rows >= 2) {
-      const int64_t fs = far_stride_bytes(p, pat, dtype);
-      int rg = (fs >= ((int64_t)4 << 20) && fs <= ((int64_t)8 << 20)) ? 8 : 2;
+      int rg = (fs >= ((int64_t)4 << 20) && fs < ((int64_t)8 << 20)) ? 8 : 2;
       while (rg < kPipeWaves && rg * c.bands < kPipeWaves) rg <<= 1;
       c.rg = rg;
       order_tiles(p, pat, (int64_t)p.B * c.HG, c);

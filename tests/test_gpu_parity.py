@@ -112,12 +112,13 @@ def test_far_free_full_tiles_at_t_2_17(layer):
 
 @pytest.mark.parametrize("b,t,h,offs", [(2, 40000, 16, (0, 1, 2, 16384)), (1, 70000, 8, (0, 32768)),
                                          (3, 16385, 8, (0, 1, 2, 16384))])
-def test_column_strip_walks(b, t, h, offs):
-    # Far offsets >= 16384 walk column strips (a workgroup on 8 consecutive
-    # tiles of one row, rows fastest): partial last rows, several head groups
-    # and batches, far-only patterns, a last row of one position.
+def test_large_far_offsets_with_partial_rows(b, t, h, offs):
+    # Far offsets >= 16384 over a few column rows: the forward's 2-row groups
+    # and the backward's row pairs with an odd row count (a pair padded with a
+    # row past T), partial last rows, a last row of one position, several
+    # head groups and batches, far-only patterns.
     q, k, v, g = _inputs(b, t, h, 64, torch.bfloat16, seed=t + h + offs[-1])
-    _close(_fused(q, k, v, offs, g), _oracle(q, k, v, offs, g), LOW_TOL, f"strips B={b} T={t} {offs}")
+    _close(_fused(q, k, v, offs, g), _oracle(q, k, v, offs, g), LOW_TOL, f"far rows B={b} T={t} {offs}")
 
 
 def test_fp16_fwd_bwd():

@@ -270,10 +270,12 @@ struct BwdChain {
   __device__ inline void prefetch(int u) {
     const int uc = clampi(u, Tm1);
     const bool live = u >= a;
-    kr[R] = load_at(k, uc);
-    vr[R] = load_at(v, uc);
-    qr[R] = load_at_if(q, uc, live);
-    gr[R] = load_at_if(go, uc, live);
+    // Own rows: k/v cached where the chain above or below reads them (first
+    // and last wave), q/dO where the chain above does (first wave).
+    kr[R] = load_at<LEFT_LDS && RIGHT_LDS>(k, uc);
+    vr[R] = load_at<LEFT_LDS && RIGHT_LDS>(v, uc);
+    qr[R] = load_at_if<LEFT_LDS>(q, uc, live);
+    gr[R] = load_at_if<LEFT_LDS>(go, uc, live);
     lr[R] = load_f32_if(lse, uc, live);
     if constexpr (!LEFT_LDS) {
       const int ul = clampi(u - F, Tm1);
@@ -562,10 +564,10 @@ struct BwdTc {
   template <int K>
   __device__ inline void prefetch(int r) {
     const int t = clampi(r * F + c, Tm1);
-    kr[K] = load_at(k, t);
-    vr[K] = load_at(v, t);
-    qr[K] = load_at(q, t);
-    gr[K] = load_at(go, t);
+    kr[K] = load_at<true>(k, t);
+    vr[K] = load_at<true>(v, t);
+    qr[K] = load_at<true>(q, t);
+    gr[K] = load_at<true>(go, t);
     lr[K] = load_f32(lse, t);
   }
 

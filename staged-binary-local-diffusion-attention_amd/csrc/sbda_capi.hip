@@ -263,8 +263,7 @@ int backward_impl(bool pro, const void* q, const int64_t* qs, const void* k, con
   hipError_t e = walk_applies(p, dtype) ? walk_backward(p, dtype, pro, st)
                                         : direct_backward(p, dtype, pro, st);
   if (e == hipSuccess && pro) {
-    e = launch_reduce_partials(p.dwq_part, pq, p.D, dwq, st);
-    if (e == hipSuccess) e = launch_reduce_partials(p.dwk_part, pk, p.D, dwk, st);
+    e = launch_reduce_partials2(p.dwq_part, pq, dwq, p.dwk_part, pk, dwk, p.D, st);
   }
   return hip_status(e, "sbda backward launch");
 }
@@ -344,8 +343,7 @@ int paths_backward_impl(const void* q, const int64_t* qs, const void* k, const i
   float* dwk_part = nullptr;
   hipError_t e = paths_backward(p, dtype, pro, ws, pq, st, &dwq_part, &dwk_part);
   if (e == hipSuccess && pro) {
-    e = launch_reduce_partials(dwq_part, pq, p.D, dwq, st);
-    if (e == hipSuccess) e = launch_reduce_partials(dwk_part, pk, p.D, dwk, st);
+    e = launch_reduce_partials2(dwq_part, pq, dwq, dwk_part, pk, dwk, p.D, st);
   }
   return hip_status(e, "sbda table-mode backward launch");
 }

@@ -336,11 +336,24 @@ void direct_partials(const Params& p, int esz, int64_t* parts_q, int64_t* parts_
 
 constexpr int kReduceBlock = 256;
 
-__global__ __launch_bounds__(kReduceBlock) void reduce_partials_kernel(const float* __restrict__ part,
-                                                                       int64_t parts, int D,
-                                                                       float* __restrict__ out) {
+// Column sums of one or two partial-row arrays ([parts, D] fp32 each): block
+// d < D sums column d of the first array, block D + d column d of the
+// second, each in a fixed order (deterministic).  The prologue backward's two
+// norm-weight gradients take one launch.
+struct PartialSet {
+  const float* part;
+  int64_t parts;
+  float* out;
+};
+
+__global__ __launch_bounds__(kReduceBlock) void reduce_partials_kernel(PartialSet a, PartialSet b,
+                                                                       int D) {
   __shared__ float buf[kReduceBlock];
-  const int d = blockIdx.x;
+  const bool second = (int)blockIdx.x >= D;
+  const float* part = second ? b.part : a.part;
+  const int64_t parts = second ? b.parts : a.parts;
+  float* out = second ? b.out : a.out;
+  const int d = second ? (int)blockIdx.x - D : (int)blockIdx.x;
   float acc = 0.f;
   for (int64_t k = threadIdx.x; k < parts; k += kReduceBlock) acc += part[k * D + d];
   buf[threadIdx.x] = acc;
@@ -353,7 +366,17 @@ __global__ __launch_bounds__(kReduceBlock) void reduce_partials_kernel(const flo
 }
 
 hipError_t launch_reduce_partials(const float* part, int64_t parts, int D, float* out, hipStream_t st) {
-  hipLaunchKernelGGL(reduce_partials_kernel, dim3((unsigned)D), dim3(kReduceBlock), 0, st, part, parts, D, out);
+  const PartialSet a{part, parts, out};
+  hipLaunchKernelGGL(reduce_partials_kernel, dim3((unsigned)D), dim3(kReduceBlock), 0, st, a, a, D);
+  return hipGetLastError();
+}
+
+hipError_t launch_reduce_partials2(const float* part_a, int64_t parts_a, float* out_a,
+                                   const float* part_b, int64_t parts_b, float* out_b, int D,
+                                   hipStream_t st) {
+  const PartialSet a{part_a, parts_a, out_a}, b{part_b, parts_b, out_b};
+  hipLaunchKernelGGL(reduce_partials_kernel, dim3(2u * (unsigned)D), dim3(kReduceBlock), 0, st, a, b,
+                     D);
   return hipGetLastError();
 }
 

@@ -57,6 +57,9 @@ hipError_t launch_forward(const Params& p, int dtype, bool prologue, hipStream_t
 hipError_t launch_backward(const Params& p, int dtype, bool prologue, hipStream_t st);
 int64_t backward_partials(const Params& p, int dtype, bool prologue, int64_t* parts_q, int64_t* parts_k);
 hipError_t launch_reduce_partials(const float* part, int64_t parts, int D, float* out, hipStream_t st);
+hipError_t launch_reduce_partials2(const float* part_a, int64_t parts_a, float* out_a,
+                                   const float* part_b, int64_t parts_b, float* out_b, int D,
+                                   hipStream_t st);
 hipError_t launch_rope_table(float* cos_out, float* sin_out, const float* inv_freq_host,
                              int64_t length, int half, hipStream_t st);
 

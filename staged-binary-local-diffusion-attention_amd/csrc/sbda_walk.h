@@ -94,12 +94,13 @@ struct ChainCfg {
 // row's far-left sources, the second row's far queries) are the own rows of
 // the workgroups beside it, fetched at about the same time on the same XCD.
 // Measured at T = 2^20 against 8-row chains on 128-position tiles: layers
-// 9-11 and 15-20 1.49-1.58 -> 1.34-1.47 ms.  Not at row strides of 4-8 MiB,
-// where pairs of rows collide in the DRAM channel mapping (layer 13: 1.54 ->
-// 1.72 ms); those keep the 8-row chains.
+// 9-11 and 15-20 1.49-1.58 -> 1.34-1.47 ms, layer 14 (8 MiB between rows)
+// 1.64 -> 1.48 ms.  Not at a row stride of 4 MiB, where pairs of rows collide
+// in the DRAM channel mapping (layer 13: 1.54 -> 1.72 ms on one box, no
+// better on another); that keeps the 8-row chains.
 inline bool chain_pairs_apply(const WalkCfg& wc, int64_t row_stride_bytes) {
   const int64_t fs = (int64_t)wc.F * row_stride_bytes;
-  return wc.F >= 128 && wc.rows >= 2 && !(fs >= ((int64_t)4 << 20) && fs <= ((int64_t)8 << 20));
+  return wc.F >= 128 && wc.rows >= 2 && !(fs >= ((int64_t)4 << 20) && fs < ((int64_t)8 << 20));
 }
 
 // Otherwise W = 8 rows (fewer when the sequence has fewer rows), at most 4

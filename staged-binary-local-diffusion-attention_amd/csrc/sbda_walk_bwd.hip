@@ -10,6 +10,16 @@ namespace walk {
 
 namespace {
 
+// Far-free walks: the rows of a tile's first four steps (a - 2 .. a + 1) are
+// the last four steps' rows of the tile before it.  A wave whose left
+// neighbour in the workgroup walks that tile leaves them in LDS, and the
+// neighbour takes its last four steps' rows from there instead of loading
+// them again (they are long gone from L2 by then).
+struct PipeStash {
+  u32x4 row[4][4][64];   // [step][k, v, q, dO][lane]
+  float lse[4][64];      // [step][lane]
+};
+
 template <typename T, int LPR, int NM, bool FAR>
 struct BwdPipe {
   static constexpr int VEC = VecOf<T>::value;
@@ -18,7 +28,10 @@ struct BwdPipe {
 
   Stream q, k, v, go, dq, dk, dv, lse;
   float scale;
-  int F, T_, Tm1, a, end;
+  int F, T_, Tm1, a, end, last;   // the walk's steps are u = a - 2 .. last
+  bool has_prev;                  // the wave before walks the tile before (stash it)
+  PipeStash* mine;                // this wave's stash (far-free)
+  const PipeStash* next;          // the next wave's stash
   Raw kr[4], vr[4];     // own k/v rotation: slot of u is R
   Raw qr[4], gr[4];     // own q/dO rotation (key finalisation reads u-2 .. u)
   float lr[4];
@@ -31,13 +44,15 @@ struct BwdPipe {
   // Rows of step u.  The two warm-up steps before the tile (u < a) only
   // provide k and v (near sources of the first queries): their queries and
   // far rows feed nothing that is stored, so those loads are skipped
-  // (load_at_if: zeros, no traffic).
+  // (load_at_if: zeros, no traffic), and so is the prefetch past the walk's
+  // last step.
   template <int R>
   __device__ inline void prefetch(int u) {
     const int uc = clampi(u, Tm1);
-    const bool live = u >= a;
-    kr[R] = load_at<!FAR>(k, uc);
-    vr[R] = load_at<!FAR>(v, uc);
+    const bool walk = u <= last;
+    const bool live = (u >= a || (!FAR && has_prev)) && walk;
+    kr[R] = load_at_if<!FAR>(k, uc, walk);
+    vr[R] = load_at_if<!FAR>(v, uc, walk);
     qr[R] = load_at_if<!FAR>(q, uc, live);
     gr[R] = load_at_if<!FAR>(go, uc, live);
     lr[R] = load_f32_if(lse, uc, live);
@@ -53,6 +68,26 @@ struct BwdPipe {
       li_[R & 1] = load_f32_if(lse, i, live);
     }
   }
+
+  // Step u's rows from the next wave's stash (slot i = u - (a + P - 2)).
+  template <int R>
+  __device__ inline void prefetch_lds(int i, int lane) {
+    kr[R] = unpack(next->row[i][0][lane]);
+    vr[R] = unpack(next->row[i][1][lane]);
+    qr[R] = unpack(next->row[i][2][lane]);
+    gr[R] = unpack(next->row[i][3][lane]);
+    lr[R] = next->lse[i][lane];
+  }
+  template <int R>
+  __device__ inline void stash(int lane) {
+    mine->row[R][0][lane] = pack(kr[R]);
+    mine->row[R][1][lane] = pack(vr[R]);
+    mine->row[R][2][lane] = pack(qr[R]);
+    mine->row[R][3][lane] = pack(gr[R]);
+    mine->lse[R][lane] = lr[R];
+  }
+  __device__ static inline u32x4 pack(const Raw& r) { return u32x4{r.w[0], r.w[1], r.w[2], r.w[3]}; }
+  __device__ static inline Raw unpack(const u32x4& x) { return Raw{{x.x, x.y, x.z, x.w}}; }
 
   // p and dS of one query from its raw operands and sources.
   __device__ inline void grads(const Raw& qq, const Raw& gg, float l, const Raw* const (&ks)[NS],
@@ -180,10 +215,12 @@ struct BwdPipe {
 
 template <typename T, int LPR, int NM, bool FAR>
 __global__ __launch_bounds__(kPipeBlock) void bwd_pipe(Params p, WalkCfg c) {
+  __shared__ PipeStash stash_lds[FAR ? 1 : kPipeWaves];
   WaveTile wt;
   wave_tile<LPR>(p, c, wt);
   constexpr int G = 64 / LPR, esz = (int)sizeof(T);
   const int h0 = wt.hg * G;
+  const int lane = threadIdx.x & 63;
   BwdPipe<T, LPR, NM, FAR> w;
   w.q = make_stream(p.q, esz, wt.b, h0, wt.hl, wt.li);
   w.k = make_stream(p.k, esz, wt.b, h0, wt.hl, wt.li);
@@ -202,8 +239,40 @@ __global__ __launch_bounds__(kPipeBlock) void bwd_pipe(Params p, WalkCfg c) {
   // Walk u = a-2 .. a+P+1 (slot of u is (u - a + 2) & 3); the trip count
   // depends only on P, the same for every wave of the workgroup.
   const int u0 = wt.a - 2, last = wt.a + c.P + 1;
+  w.last = last;
+  bool next_adj = false;
+  w.has_prev = false;
+  if constexpr (!FAR) {
+    // Neighbours in the workgroup on the tiles just before / after this one.
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int64_t n = xcd_remap(blockIdx.x, gridDim.x) * c.waves + wv;
+    int b2, hg2, a2;
+    if (wt.a < p.T && wv + 1 < c.waves && decode_tile(p, c, n + 1, b2, hg2, a2))
+      next_adj = b2 == wt.b && hg2 == wt.hg && a2 == wt.a + c.P;
+    if (wt.a < p.T && wv > 0 && decode_tile(p, c, n - 1, b2, hg2, a2))
+      w.has_prev = b2 == wt.b && hg2 == wt.hg && a2 + c.P == wt.a;
+    w.mine = &stash_lds[wv];
+    w.next = &stash_lds[wv + 1 < kPipeWaves ? wv + 1 : wv];
+  }
   w.template prefetch<0>(u0);
-  for (int u = u0; u <= last; u += 4) {
+  // First trip: its rows (a - 2 .. a + 1) also go to the stash when the wave
+  // before walks the tile before.
+  __syncthreads();
+  w.template prefetch<1>(u0 + 1);
+  w.template compute<0>(u0);
+  if (!FAR && w.has_prev) w.template stash<0>(lane);
+  w.template prefetch<2>(u0 + 2);
+  w.template compute<1>(u0 + 1);
+  if (!FAR && w.has_prev) w.template stash<1>(lane);
+  w.template prefetch<3>(u0 + 3);
+  w.template compute<2>(u0 + 2);
+  if (!FAR && w.has_prev) w.template stash<2>(lane);
+  w.template prefetch<0>(u0 + 4);
+  w.template compute<3>(u0 + 3);
+  if (!FAR && w.has_prev) w.template stash<3>(lane);
+  // Middle trips.
+  const int ls = wt.a + c.P - 2;   // first of the last four steps
+  for (int u = u0 + 4; u < ls - 4; u += 4) {
     __syncthreads();
     w.template prefetch<1>(u + 1);
     w.template compute<0>(u);
@@ -213,6 +282,46 @@ __global__ __launch_bounds__(kPipeBlock) void bwd_pipe(Params p, WalkCfg c) {
     w.template compute<2>(u + 2);
     w.template prefetch<0>(u + 4);
     w.template compute<3>(u + 3);
+  }
+  // Last two trips (steps ls - 4 .. ls + 3): the last four steps' rows come
+  // from the next wave's stash when it walks the next tile.
+  const int u = ls - 4;
+  if (!FAR && next_adj) {
+    __syncthreads();
+    w.template prefetch<1>(u + 1);
+    w.template compute<0>(u);
+    w.template prefetch<2>(u + 2);
+    w.template compute<1>(u + 1);
+    w.template prefetch<3>(u + 3);
+    w.template compute<2>(u + 2);
+    w.template prefetch_lds<0>(0, lane);
+    w.template compute<3>(u + 3);
+    __syncthreads();
+    w.template prefetch_lds<1>(1, lane);
+    w.template compute<0>(ls);
+    w.template prefetch_lds<2>(2, lane);
+    w.template compute<1>(ls + 1);
+    w.template prefetch_lds<3>(3, lane);
+    w.template compute<2>(ls + 2);
+    w.template compute<3>(ls + 3);
+  } else {
+    __syncthreads();
+    w.template prefetch<1>(u + 1);
+    w.template compute<0>(u);
+    w.template prefetch<2>(u + 2);
+    w.template compute<1>(u + 1);
+    w.template prefetch<3>(u + 3);
+    w.template compute<2>(u + 2);
+    w.template prefetch<0>(ls);
+    w.template compute<3>(u + 3);
+    __syncthreads();
+    w.template prefetch<1>(ls + 1);
+    w.template compute<0>(ls);
+    w.template prefetch<2>(ls + 2);
+    w.template compute<1>(ls + 1);
+    w.template prefetch<3>(ls + 3);
+    w.template compute<2>(ls + 2);
+    w.template compute<3>(ls + 3);
   }
 }
 
@@ -271,7 +380,10 @@ struct BwdChain {
     const int uc = clampi(u, Tm1);
     const bool live = u >= a;
     // Own rows: k/v cached where the chain above or below reads them (first
-    // and last wave), q/dO where the chain above does (first wave).
+    // and last wave), q/dO where the chain above does (first wave).  (Buffer
+    // loads here, to skip the prefetch past the last step, measured 5-10%
+    // slower: four more buffer resources on a kernel that already spills
+    // scalar registers.)
     kr[R] = load_at<LEFT_LDS && RIGHT_LDS>(k, uc);
     vr[R] = load_at<LEFT_LDS && RIGHT_LDS>(v, uc);
     qr[R] = load_at_if<LEFT_LDS>(q, uc, live);
@@ -561,14 +673,18 @@ struct BwdTc {
   float p0[4], d0[4];               // own query's self-slot (p, scale dS) by row & 3
   float pf[4], df[4];               // own query's far-slot (p, scale dS) by row & 3
 
+  // Rows r0 - 1 .. r0 + R are used (sources of the first row, queries of the
+  // last keys); the walk's alignment steps before and after them load
+  // nothing (load_at_if: zeros, no traffic).
   template <int K>
   __device__ inline void prefetch(int r) {
     const int t = clampi(r * F + c, Tm1);
-    kr[K] = load_at<true>(k, t);
-    vr[K] = load_at<true>(v, t);
-    qr[K] = load_at<true>(q, t);
-    gr[K] = load_at<true>(go, t);
-    lr[K] = load_f32(lse, t);
+    const bool used = r >= r0 - 1 && r <= r0 + R;
+    kr[K] = load_at_if<true>(k, t, used);
+    vr[K] = load_at_if<true>(v, t, used);
+    qr[K] = load_at_if<true>(q, t, used);
+    gr[K] = load_at_if<true>(go, t, used);
+    lr[K] = load_f32_if(lse, t, used);
   }
 
   __device__ static inline u32x4 pack(const Raw& x) { return u32x4{x.w[0], x.w[1], x.w[2], x.w[3]}; }
@@ -822,10 +938,12 @@ hipError_t launch_bwd(const Params& p, const WalkCfg& c, const Pattern& pat, int
       return pat.nm == 7 ? launch_tc<T, L, 7, 8>(p, c, st) : launch_tc<T, L, 1, 8>(p, c, st);
     }
     const dim3 grid((unsigned)c.nwg), block(kPipeBlock);
+    // The far-free walks hold their stashes in static LDS (136 KiB: one
+    // workgroup per CU without the extra allocation).
     if (pat.far == 0 && pat.nm == 3)
-      hipLaunchKernelGGL((bwd_pipe<T, L, 3, false>), grid, block, kPipeLds, st, p, c);
+      hipLaunchKernelGGL((bwd_pipe<T, L, 3, false>), grid, block, 0, st, p, c);
     else if (pat.far == 0 && pat.nm == 5)
-      hipLaunchKernelGGL((bwd_pipe<T, L, 5, false>), grid, block, kPipeLds, st, p, c);
+      hipLaunchKernelGGL((bwd_pipe<T, L, 5, false>), grid, block, 0, st, p, c);
     else if (pat.far != 0 && pat.nm == 7)
       hipLaunchKernelGGL((bwd_pipe<T, L, 7, true>), grid, block, kPipeLds, st, p, c);
     else if (pat.far != 0 && pat.nm == 1)

@@ -552,10 +552,12 @@ struct BwdChain {
   }
 
   __device__ inline void walk(int steps_from) {
-    // u = a-2 .. a+P+1 for every wave of the workgroup (same trip count).
+    // u = a-2 .. a+P+1 for every wave of the workgroup (same trip count); the
+    // last trip issues no prefetch past the walk.
     const int u0 = steps_from;
     prefetch<0>(u0);
-    for (int u = u0; u <= u0 + (end_u - u0); u += 4) {
+    int u = u0;
+    for (; u + 3 < end_u; u += 4) {
       prefetch<1>(u + 1);
       compute<0>(u);
       prefetch<2>(u + 2);
@@ -565,6 +567,13 @@ struct BwdChain {
       prefetch<0>(u + 4);
       compute<3>(u + 3);
     }
+    prefetch<1>(u + 1);
+    compute<0>(u);
+    prefetch<2>(u + 2);
+    compute<1>(u + 1);
+    prefetch<3>(u + 3);
+    compute<2>(u + 2);
+    compute<3>(u + 3);
   }
   int end_u;
 };

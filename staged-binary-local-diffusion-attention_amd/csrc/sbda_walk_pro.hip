@@ -457,8 +457,11 @@ struct BwdKPro : ProBase<T, LPR> {
 // Four steps per trip with one barrier (the workgroup walks in lockstep).
 template <typename W>
 __device__ inline void walk4(W& w, int first, int last) {
+  // Steps first .. last (a multiple of 4 of them); the last trip issues no
+  // prefetch past the walk.
   w.template prefetch<0>(first);
-  for (int u = first; u <= last; u += 4) {
+  int u = first;
+  for (; u + 3 < last; u += 4) {
     __syncthreads();
     w.template prefetch<1>(u + 1);
     w.template compute<0>(u);
@@ -469,6 +472,14 @@ __device__ inline void walk4(W& w, int first, int last) {
     w.template prefetch<0>(u + 4);
     w.template compute<3>(u + 3);
   }
+  __syncthreads();
+  w.template prefetch<1>(u + 1);
+  w.template compute<0>(u);
+  w.template prefetch<2>(u + 2);
+  w.template compute<1>(u + 1);
+  w.template prefetch<3>(u + 3);
+  w.template compute<2>(u + 2);
+  w.template compute<3>(u + 3);
 }
 
 __device__ inline int64_t pipe_wave_id(const WalkCfg& c) {
@@ -996,9 +1007,11 @@ struct BwdChainPro : ProBase<T, LPR> {
   }
 
   __device__ inline void walk(int u0, int end_u) {
-    // u = a-2 .. a+P+1 for every wave of the workgroup (same trip count).
+    // u = a-2 .. a+P+1 for every wave of the workgroup (same trip count); the
+    // last trip issues no prefetch past the walk.
     this->template prefetch<0>(u0);
-    for (int u = u0; u <= end_u; u += 4) {
+    int u = u0;
+    for (; u + 3 < end_u; u += 4) {
       stash<0>();
       this->template prefetch<1>(u + 1);
       this->template compute<0>(u);
@@ -1012,6 +1025,17 @@ struct BwdChainPro : ProBase<T, LPR> {
       this->template prefetch<0>(u + 4);
       this->template compute<3>(u + 3);
     }
+    stash<0>();
+    this->template prefetch<1>(u + 1);
+    this->template compute<0>(u);
+    stash<1>();
+    this->template prefetch<2>(u + 2);
+    this->template compute<1>(u + 1);
+    stash<2>();
+    this->template prefetch<3>(u + 3);
+    this->template compute<2>(u + 2);
+    stash<3>();
+    this->template compute<3>(u + 3);
   }
 };
 

@@ -1321,6 +1321,76 @@ struct FwdChainPro : ProBase<T, LPR> {
   }
 };
 
+// The extra wave of a forward chain: it walks the row before the block and
+// only loads, ropes and publishes its k and v rows -- the far-left sources of
+// the block's first row -- so that every wave that computes takes its far
+// sources from LDS and the lockstep steps are not held by one wave doing a
+// third prologue.
+template <typename T, int LPR>
+struct FwdChainLoader : ProBase<T, LPR> {
+  using B_ = ProBase<T, LPR>;
+  using B_::VEC;
+  using B_::HV;
+  using Slot = FwdChainSlot<VecOf<T>::value>;
+
+  SplitStream k, v;
+  int lane;
+  Slot* mine;
+  Raw kraw[2], vraw[2];
+  float cc[2][HV], ss[2][HV];
+
+  template <int R>
+  __device__ inline void prefetch(int t) {
+    const int tc = clampi(t, this->Tm1);
+    kraw[R & 1] = load_split(k, tc);
+    vraw[R & 1] = load_split(v, tc);
+    this->cs(tc, cc[R & 1], ss[R & 1]);
+  }
+
+  template <int R>
+  __device__ inline void compute(int, bool) {
+    float kq[VEC];
+    this->rope(kraw[R & 1], this->wk, cc[R & 1], ss[R & 1], kq);
+    put_rows<VEC>(mine->kf[R & 1], lane, kq);
+    mine->vf[R & 1][lane] = pack_raw(vraw[R & 1]);
+    __syncthreads();
+  }
+};
+
+template <typename T, int LPR>
+__device__ inline void fwd_chain_loader(const Params& p, const ChainCfg& c,
+                                        FwdChainSlot<VecOf<T>::value>* lds, int b, int hg, int a) {
+  constexpr int esz = (int)sizeof(T);
+  const int lane = threadIdx.x & 63, hl = lane / LPR, li = lane % LPR;
+  const int h0 = hg * (64 / LPR);
+  FwdChainLoader<T, LPR> x;
+  x.init(p, li);
+  x.k = make_split(p.k, esz, b, h0, hl, li, p.D, x.HV);
+  x.v = make_split(p.v, esz, b, h0, hl, li, p.D, x.HV);
+  x.lane = lane;
+  x.mine = lds;
+  const int t0 = a - 2;
+  x.template prefetch<0>(t0);
+  int t = t0;
+  for (; t + 4 < a + c.P; t += 4) {
+    x.template prefetch<1>(t + 1);
+    x.template compute<0>(t, false);
+    x.template prefetch<2>(t + 2);
+    x.template compute<1>(t + 1, false);
+    x.template prefetch<3>(t + 3);
+    x.template compute<2>(t + 2, false);
+    x.template prefetch<0>(t + 4);
+    x.template compute<3>(t + 3, false);
+  }
+  x.template prefetch<1>(t + 1);
+  x.template compute<0>(t, false);
+  x.template prefetch<2>(t + 2);
+  x.template compute<1>(t + 1, false);
+  x.template prefetch<3>(t + 3);
+  x.template compute<2>(t + 2, false);
+  x.template compute<3>(t + 3, false);
+}
+
 template <typename T, int LPR, int NM, bool LEFT_LDS, int W>
 __device__ inline void fwd_chain_wave(const Params& p, const ChainCfg& c,
                                       FwdChainSlot<VecOf<T>::value>* lds, int w, int b, int hg,
@@ -1345,7 +1415,8 @@ __device__ inline void fwd_chain_wave(const Params& p, const ChainCfg& c,
   // count depends only on P.
   const int t0 = a - 2;
   x.template prefetch<0>(t0);
-  for (int t = t0; t < a + c.P; t += 4) {
+  int t = t0;
+  for (; t + 4 < a + c.P; t += 4) {
     x.template prefetch<1>(t + 1);
     x.template compute<0>(t, t >= a && t < end);
     x.template prefetch<2>(t + 2);
@@ -1355,14 +1426,32 @@ __device__ inline void fwd_chain_wave(const Params& p, const ChainCfg& c,
     x.template prefetch<0>(t + 4);
     x.template compute<3>(t + 3, t + 3 >= a && t + 3 < end);
   }
+  // Last trip: no prefetch past the walk.
+  x.template prefetch<1>(t + 1);
+  x.template compute<0>(t, t >= a && t < end);
+  x.template prefetch<2>(t + 2);
+  x.template compute<1>(t + 1, t + 1 >= a && t + 1 < end);
+  x.template prefetch<3>(t + 3);
+  x.template compute<2>(t + 2, t + 2 >= a && t + 2 < end);
+  x.template compute<3>(t + 3, t + 3 >= a && t + 3 < end);
 }
 
+// 8-row chains run with the loader wave (layers 5-15 of the prologue forward
+// at T = 2^20: 0.96-0.97x the time); the shorter chains at row strides of
+// 32 MiB and more measured 5-13% slower with it and keep their first wave
+// loading its own far rows.
+template <int W>
+constexpr int fwd_chain_loader_waves() { return W == 8 ? 1 : 0; }
+
 template <typename T, int LPR, int NM, int W>
-__global__ __launch_bounds__(64 * W) void fwd_chain_pro(Params p, ChainCfg c) {
-  __shared__ FwdChainSlot<VecOf<T>::value> lds[W];
-  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  // Workgroup -> (batch, head group, band, row block), XCD-contiguous; wave w
-  // -> row w of the block.
+__global__ __launch_bounds__(64 * (W + fwd_chain_loader_waves<W>())) void fwd_chain_pro(Params p,
+                                                                                       ChainCfg c) {
+  constexpr int LW = fwd_chain_loader_waves<W>();
+  __shared__ FwdChainSlot<VecOf<T>::value> lds[W + LW];
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  // Workgroup -> (batch, head group, band, row block), XCD-contiguous; with
+  // the loader, wave 0 -> the row before the block and wave w >= 1 -> row
+  // w - 1; without, wave w -> row w.
   int64_t g = xcd_remap(blockIdx.x, gridDim.x);
   const int rb = (int)(g % c.blocks);
   g /= c.blocks;
@@ -1370,13 +1459,19 @@ __global__ __launch_bounds__(64 * W) void fwd_chain_pro(Params p, ChainCfg c) {
   g /= c.bands;
   const int hg = (int)(g % c.HG);
   const int b = (int)(g / c.HG);
-  const int r = rb * W + w;
+  const int r = rb * W + wv - LW;
   const int64_t a64 = (int64_t)r * c.F + (int64_t)cb * c.P;
-  const int a = (r < c.rows && a64 < p.T) ? (int)a64 : p.T;
-  if (w == 0)
-    fwd_chain_wave<T, LPR, NM, false, W>(p, c, lds, w, b, hg, a);
-  else
-    fwd_chain_wave<T, LPR, NM, true, W>(p, c, lds, w, b, hg, a);
+  if (LW && wv == 0) {
+    // Row rb * W - 1 (before the sequence for the first block: its clamped
+    // rows are the sources of positions t - F < 0, which no query uses).
+    fwd_chain_loader<T, LPR>(p, c, lds, b, hg, (int)a64);
+  } else {
+    const int a = (r < c.rows && a64 < p.T) ? (int)a64 : p.T;
+    if (LW || wv > 0)
+      fwd_chain_wave<T, LPR, NM, true, W>(p, c, lds, wv, b, hg, a);
+    else
+      fwd_chain_wave<T, LPR, NM, false, W>(p, c, lds, wv, b, hg, a);
+  }
 }
 
 }  // namespace
@@ -1389,7 +1484,7 @@ hipError_t pro_pattern(bool fwd, const Params& p, const WalkCfg& c, int dtype, h
       if (c.column) {
         const ChainCfg cc = make_chain_cfg(p.B, p.q.st * (int64_t)sizeof(T), c);
         if (cc.nwg <= 0) return hipErrorInvalidValue;
-        const dim3 cgrid((unsigned)cc.nwg), cblock(64 * cc.W);
+        const dim3 cgrid((unsigned)cc.nwg), cblock(64 * (cc.W + (cc.W == 8 ? 1 : 0)));
         switch (cc.W) {
           case 8: hipLaunchKernelGGL((fwd_chain_pro<T, LPR, NM, 8>), cgrid, cblock, 0, st, p, cc); break;
           case 4: hipLaunchKernelGGL((fwd_chain_pro<T, LPR, NM, 4>), cgrid, cblock, 0, st, p, cc); break;

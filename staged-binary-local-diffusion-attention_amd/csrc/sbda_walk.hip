@@ -104,9 +104,12 @@ WalkCfg launch_cfg(const Params& p, int dtype, const Pattern& pat, int lpr, bool
     // at least 4 rows, pairs of 32-position tiles (2 rows x 4 bands of 32)
     // measured faster than 64 (layers 14-19: 0.76-0.80 against 0.75-0.87 ms,
     // two boxes); not with 2 rows (layer 20: 0.80 against 0.74 ms).
+    // At F = 128, 64-position tiles leave 2 bands (a group of 4 rows x 2
+    // bands); 32-position tiles keep the 2-row groups (layer 8: 0.787 against
+    // 0.801 ms in the sweep below).
     const int64_t fs = far_stride_bytes(p, pat, dtype);
     const int64_t rows = (p.T + pat.far - 1) / pat.far;
-    const bool narrow = fs >= ((int64_t)8 << 20) && rows >= 4;
+    const bool narrow = (fs >= ((int64_t)8 << 20) && rows >= 4) || pat.far < 4 * 64;
     WalkCfg c = make_pipe_cfg(p, lpr, pat, narrow ? 32 : 64);
     if (c.column && c.rows >= 2) {
       int rg = (fs >= ((int64_t)4 << 20) && fs < ((int64_t)8 << 20)) ? 8 : 2;

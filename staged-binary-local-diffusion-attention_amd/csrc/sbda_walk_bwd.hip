@@ -1,7 +1,8 @@
 // Backward walks (gather form, every gradient row written once, no atomics):
-// independent lockstep walks (bwd_pipe), chained column walks (bwd_chain) and
-// transposed chains for far offsets 4 and 8 (bwd_tc).  Reference semantics:
-// the key-centric backward specified by BiAttn/sbda_triton.py:507-671.
+// independent lockstep walks (bwd_pipe; bwd_fr4 for far offset 4), chained
+// column walks (bwd_chain) and transposed chains for far offset 8 (bwd_tc).
+// Reference semantics: the key-centric backward specified by
+// BiAttn/sbda_triton.py:507-671.
 
 #include "sbda_walk.h"
 
@@ -325,6 +326,179 @@ __global__ __launch_bounds__(kPipeBlock) void bwd_pipe(Params p, WalkCfg c) {
   }
 }
 
+// ====================================== rotation backward (far offset 4)
+//
+// For F = 4 the far source of query u is the wave's own row u - 4 and the far
+// query of key j is its own query j + 4: with rotations 6 deep (k/v for the
+// query's sources, q/dO for the key's queries) a wave walks its tile alone,
+// as the far-free walk does (8-wave lockstep groups over consecutive tiles);
+// key j is finished at step j + 4.  Steps u = a - 4 .. a + P + 3 (the first
+// four load only k/v), in trips of 6.  Same sums in the same order as the
+// transposed chain (outputs bitwise identical); at T = 2^20, layer 3: 1.52 ->
+// 1.39 ms.  (F = 8 would need rotations 10 deep: more registers than a lane
+// has; it keeps the transposed chain.)
+
+template <typename T, int LPR, int NM>
+struct BwdFr4 {
+  static constexpr int VEC = VecOf<T>::value;
+  static constexpr int NN = NearSet<NM>::count;
+  static constexpr int NS = NN + 1;
+  static constexpr int FR = 4, RD = 6;
+
+  Stream q, k, v, go, dq, dk, dv, lse;
+  float scale;
+  int T_, Tm1, a, end, last;
+  Raw kr[RD], vr[RD], qr[RD], gr[RD];
+  float lr[RD];
+  float sp[RD][3], sd[RD][3];
+
+  template <int S>
+  __device__ inline void prefetch(int u) {
+    const int uc = clampi(u, Tm1);
+    const bool walk = u <= last;
+    const bool live = u >= a && walk;
+    kr[S] = load_at_if<true>(k, uc, walk);
+    vr[S] = load_at_if<true>(v, uc, walk);
+    qr[S] = load_at_if<true>(q, uc, live);
+    gr[S] = load_at_if<true>(go, uc, live);
+    lr[S] = load_f32_if(lse, uc, live);
+  }
+
+  template <int R>
+  __device__ inline void compute(int u) {
+    const Raw* ks[NS];
+    const Raw* vs[NS];
+    bool ok[NS];
+    int idx = 0;
+#pragma unroll
+    for (int n = 0; n < 3; ++n) {
+      if (NM & (1 << n)) {
+        ks[idx] = &kr[(R + RD - n) % RD];
+        vs[idx] = &vr[(R + RD - n) % RD];
+        ok[idx] = u - n >= 0;
+        ++idx;
+      }
+    }
+    constexpr int sf = (R + RD - FR) % RD;
+    ks[NS - 1] = &kr[sf];
+    vs[NS - 1] = &vr[sf];
+    ok[NS - 1] = u - FR >= 0;
+    float pp[NS], ds[NS];
+    {
+      float dp[NS];
+      float delta = 0.f;
+#pragma unroll
+      for (int s_ = 0; s_ < NS; ++s_) {
+        const float sc = row_sum<LPR>(dot_raw<T>(qr[R], *ks[s_])) * scale;
+        dp[s_] = row_sum<LPR>(dot_raw<T>(gr[R], *vs[s_]));
+        pp[s_] = ok[s_] ? fast_exp(sc - lr[R]) : 0.f;
+        delta = __builtin_fmaf(pp[s_], dp[s_], delta);
+      }
+#pragma unroll
+      for (int s_ = 0; s_ < NS; ++s_) ds[s_] = pp[s_] * (dp[s_] - delta);
+    }
+#pragma unroll
+    for (int n = 0; n < NN; ++n) {
+      sp[R][n] = pp[n];
+      sd[R][n] = ds[n] * scale;
+    }
+    if (u >= a && u < end) {
+      float g[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) g[e] = 0.f;
+#pragma unroll
+      for (int s_ = 0; s_ < NS; ++s_) {
+        float kx[VEC];
+        widen<T>(*ks[s_], kx);
+        const float c = ds[s_] * scale;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) g[e] = __builtin_fmaf(c, kx[e], g[e]);
+      }
+      store_at<T>(dq, u, g);
+    }
+    // Key j = u - 4: near queries j + n, far query u.
+    const int j = u - FR;
+    if (j >= a && j < end) {
+      float ak[VEC], av[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) { ak[e] = 0.f; av[e] = 0.f; }
+      int i2 = 0;
+#pragma unroll
+      for (int n = 0; n < 3; ++n) {
+        if (NM & (1 << n)) {
+          const int slot = (R + RD - FR + n) % RD;   // slot of query j + n
+          const bool there = j + n < T_;
+          const float cs = there ? sd[slot][i2] : 0.f;
+          const float cp = there ? sp[slot][i2] : 0.f;
+          float qx[VEC], gx[VEC];
+          widen<T>(qr[slot], qx);
+          widen<T>(gr[slot], gx);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            ak[e] = __builtin_fmaf(cs, qx[e], ak[e]);
+            av[e] = __builtin_fmaf(cp, gx[e], av[e]);
+          }
+          ++i2;
+        }
+      }
+      const bool there = u < T_;
+      const float cs = there ? ds[NS - 1] * scale : 0.f;
+      const float cp = there ? pp[NS - 1] : 0.f;
+      float qx[VEC], gx[VEC];
+      widen<T>(qr[R], qx);
+      widen<T>(gr[R], gx);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        ak[e] = __builtin_fmaf(cs, qx[e], ak[e]);
+        av[e] = __builtin_fmaf(cp, gx[e], av[e]);
+      }
+      store_at<T>(dk, j, ak);
+      store_at<T>(dv, j, av);
+    }
+  }
+
+  template <int R>
+  __device__ inline void steps(int u) {
+    if constexpr (R < RD) {
+      prefetch<(R + 1) % RD>(u + R + 1);
+      compute<R>(u + R);
+      steps<R + 1>(u);
+    }
+  }
+};
+
+template <typename T, int LPR, int NM>
+__global__ __launch_bounds__(kPipeBlock) void bwd_fr4(Params p, WalkCfg c) {
+  WaveTile wt;
+  wave_tile<LPR>(p, c, wt);
+  constexpr int G = 64 / LPR, esz = (int)sizeof(T);
+  const int h0 = wt.hg * G;
+  using W = BwdFr4<T, LPR, NM>;
+  W w;
+  w.q = make_stream(p.q, esz, wt.b, h0, wt.hl, wt.li);
+  w.k = make_stream(p.k, esz, wt.b, h0, wt.hl, wt.li);
+  w.v = make_stream(p.v, esz, wt.b, h0, wt.hl, wt.li);
+  w.go = make_stream(p.dout, esz, wt.b, h0, wt.hl, wt.li);
+  w.dq = make_stream(p.dq, esz, wt.b, h0, wt.hl, wt.li);
+  w.dk = make_stream(p.dk, esz, wt.b, h0, wt.hl, wt.li);
+  w.dv = make_stream(p.dv, esz, wt.b, h0, wt.hl, wt.li);
+  w.lse = lse_stream(p, wt.b, h0, wt.hl);
+  w.scale = p.scale;
+  w.T_ = p.T;
+  w.Tm1 = p.T - 1;
+  w.a = wt.a;
+  w.end = min(wt.a + c.P, p.T);
+  const int u0 = wt.a - W::FR;
+  w.last = wt.a + c.P + W::FR - 1;
+  // Trips of RD steps from u0 (slot of u is (u - u0) % RD); the trip count
+  // depends only on P.
+  w.template prefetch<0>(u0);
+  for (int u = u0; u <= w.last; u += W::RD) {
+    __syncthreads();
+    w.template steps<0>(u);
+  }
+}
+
 // ============================================== chained backward (far >= tile)
 //
 // With the far offset F a multiple of the tile P, the tiles of one band form
@@ -640,7 +814,7 @@ __global__ __launch_bounds__(64 * W) void bwd_chain(Params p, ChainCfg c) {
   }
 }
 
-// ============================================= transposed chain (far = 4, 8)
+// ============================================ transposed chain (far = 8)
 //
 // For a small far offset F the far rows are F steps back in a wave's own walk
 // -- evicted from L2 by then.  Here the sequence is seen as rows of F
@@ -941,12 +1115,14 @@ hipError_t launch_bwd(const Params& p, const WalkCfg& c, const Pattern& pat, int
     constexpr int L = decltype(lprc)::value;
     if (pat.far != 0 && c.column)
       return pat.nm == 7 ? launch_chain<T, L, 7>(p, c, st) : launch_chain<T, L, 1>(p, c, st);
-    if ((pat.far == 4 || pat.far == 8) && !c.column) {
-      if (pat.far == 4)
-        return pat.nm == 7 ? launch_tc<T, L, 7, 4>(p, c, st) : launch_tc<T, L, 1, 4>(p, c, st);
-      return pat.nm == 7 ? launch_tc<T, L, 7, 8>(p, c, st) : launch_tc<T, L, 1, 8>(p, c, st);
-    }
     const dim3 grid((unsigned)c.nwg), block(kPipeBlock);
+    if (pat.far == 4 && !c.column) {
+      if (pat.nm == 7) hipLaunchKernelGGL((bwd_fr4<T, L, 7>), grid, block, kPipeLds, st, p, c);
+      else hipLaunchKernelGGL((bwd_fr4<T, L, 1>), grid, block, kPipeLds, st, p, c);
+      return hipGetLastError();
+    }
+    if (pat.far == 8 && !c.column)
+      return pat.nm == 7 ? launch_tc<T, L, 7, 8>(p, c, st) : launch_tc<T, L, 1, 8>(p, c, st);
     // The far-free walks hold their stashes in static LDS (136 KiB: one
     // workgroup per CU without the extra allocation).
     if (pat.far == 0 && pat.nm == 3)

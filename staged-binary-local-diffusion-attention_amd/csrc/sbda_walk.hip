@@ -117,6 +117,7 @@ WalkCfg launch_cfg(const Params& p, int dtype, const Pattern& pat, int lpr, bool
       c.rg = rg;
       order_tiles(p, pat, (int64_t)p.B * c.HG, c);
     }
+    c.xs = xcd_stagger(c.nwg, fs);
     return c;
   }
   // The far-free forward takes 64-position tiles: its tiles load the 2 rows
@@ -140,6 +141,9 @@ WalkCfg launch_cfg(const Params& p, int dtype, const Pattern& pat, int lpr, bool
     c.rg = 4;
     order_tiles(p, pat, (int64_t)p.B * c.HG, c);
   }
+  // The prologue walks keep the plain XCD order (the stagger was measured on
+  // the plain walks only).
+  if (!pro) c.xs = xcd_stagger(c.nwg, far_stride_bytes(p, pat, dtype));
   return c;
 }
 

@@ -246,7 +246,7 @@ __global__ __launch_bounds__(kPipeBlock) void bwd_pipe(Params p, WalkCfg c) {
   if constexpr (!FAR) {
     // Neighbours in the workgroup on the tiles just before / after this one.
     const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int64_t n = xcd_remap(blockIdx.x, gridDim.x) * c.waves + wv;
+    const int64_t n = xcd_remap(blockIdx.x, gridDim.x, c.xs) * c.waves + wv;
     int b2, hg2, a2;
     if (wt.a < p.T && wv + 1 < c.waves && decode_tile(p, c, n + 1, b2, hg2, a2))
       next_adj = b2 == wt.b && hg2 == wt.hg && a2 == wt.a + c.P;
@@ -786,7 +786,7 @@ __global__ __launch_bounds__(64 * W) void bwd_chain(Params p, ChainCfg c) {
   const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   // Workgroup -> (batch, head group, band group, row block), XCD-contiguous;
   // wave w -> row w % L of the block, band w / L of the group.
-  int64_t g = xcd_remap(blockIdx.x, gridDim.x);
+  int64_t g = xcd_remap(blockIdx.x, gridDim.x, c.xs);
   const int rb = (int)(g % c.blocks);
   g /= c.blocks;
   const int bgi = (int)(g % c.bgroups);
@@ -1076,8 +1076,9 @@ __global__ __launch_bounds__(64 * F) void bwd_tc(Params p, TcCfg cfg) {
 template <typename T, int LPR, int NM>
 hipError_t launch_chain(const Params& p, const WalkCfg& wc, hipStream_t st) {
   const int64_t stride = p.q.st * (int64_t)sizeof(T);
-  const ChainCfg c = make_chain_cfg(p.B, stride, wc, chain_pairs_apply(wc, stride));
+  ChainCfg c = make_chain_cfg(p.B, stride, wc, chain_pairs_apply(wc, stride));
   if (c.nwg <= 0) return hipErrorInvalidValue;
+  c.xs = xcd_stagger(c.nwg, (int64_t)c.F * stride);
   const dim3 grid((unsigned)c.nwg), block(64 * c.W);
   switch (c.W) {
     case 8: hipLaunchKernelGGL((bwd_chain<T, LPR, NM, 8>), grid, block, 0, st, p, c); break;

@@ -193,7 +193,7 @@ __global__ __launch_bounds__(kPipeBlock) void fwd_pipe(Params p, WalkCfg c) {
     const int d = (c.HG == 1 && !c.column) ? 1 : 0;
     w.has_prev = w.next_adj = false;
     if (d && a < p.T) {
-      const int64_t n = xcd_remap(blockIdx.x, gridDim.x) * c.waves + wv;
+      const int64_t n = xcd_remap(blockIdx.x, gridDim.x, c.xs) * c.waves + wv;
       int b2, hg2, a2;
       if (wv + d < c.waves && decode_tile(p, c, n + d, b2, hg2, a2))
         w.next_adj = b2 == wt.b && a2 == a + c.P;

@@ -68,14 +68,14 @@ void order_tiles(const Params& p, const Pattern& pat, int64_t lanes_rows, WalkCf
 // (column order, far rows one column row away); halved (not below 16) while
 // the grid has fewer than 256 full workgroups.
 WalkCfg make_pipe_cfg(const Params& p, int lpr, const Pattern& pat, int max_col_tile,
-                      int lin_tile = 32) {
+                      int lin_tile = 32, int min_tile = 16) {
   WalkCfg c{};
   c.waves = kPipeWaves;
   c.HG = p.H / (64 / lpr);
   const int64_t lanes_rows = (int64_t)p.B * c.HG;
   const bool pow2far = pat.far >= 16 && (pat.far & (pat.far - 1)) == 0;
   int P = pow2far ? min(max_col_tile, pat.far) : lin_tile;
-  while (P > 16 && lanes_rows * ((p.T + P - 1) / P) < 256 * kPipeWaves) P >>= 1;
+  while (P > min_tile && lanes_rows * ((p.T + P - 1) / P) < 256 * kPipeWaves) P >>= 1;
   c.P = P;
   order_tiles(p, pat, lanes_rows, c);
   return c;
@@ -136,7 +136,9 @@ WalkCfg launch_cfg(const Params& p, int dtype, const Pattern& pat, int lpr, bool
     if (probe.column && walk::chain_pairs_apply(probe, far_stride_bytes(p, pat, dtype) / pat.far))
       col_tile = pat.far >= 256 ? 64 : 32;
   }
-  WalkCfg c = make_pipe_cfg(p, lpr, pat, col_tile, lin);
+  // The rotation backward at F = 4 keeps 32-position tiles (its trip layout).
+  const int min_tile = (!fwd && !pro && pat.far == 4) ? 32 : 16;
+  WalkCfg c = make_pipe_cfg(p, lpr, pat, col_tile, lin, min_tile);
   if ((fwd || pro) && c.column && c.rows > 4 && far_stride_bytes(p, pat, dtype) >= kBigStride) {
     c.rg = 4;
     order_tiles(p, pat, (int64_t)p.B * c.HG, c);

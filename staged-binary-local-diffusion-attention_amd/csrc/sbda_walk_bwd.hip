@@ -348,6 +348,8 @@ struct BwdFr4 {
   Stream q, k, v, go, dq, dk, dv, lse;
   float scale;
   int T_, Tm1, a, end, last;
+  PipeStash* mine;          // this wave's first four rows, for the wave before
+  const PipeStash* next;    // the next wave's first four rows
   Raw kr[RD], vr[RD], qr[RD], gr[RD];
   float lr[RD];
   float sp[RD][3], sd[RD][3];
@@ -363,6 +365,26 @@ struct BwdFr4 {
     gr[S] = load_at_if<true>(go, uc, live);
     lr[S] = load_f32_if(lse, uc, live);
   }
+  // Row a + P + i (the next tile's row i) from the next wave's stash.
+  template <int S>
+  __device__ inline void prefetch_lds(int i, int lane) {
+    kr[S] = unpack(next->row[i][0][lane]);
+    vr[S] = unpack(next->row[i][1][lane]);
+    qr[S] = unpack(next->row[i][2][lane]);
+    gr[S] = unpack(next->row[i][3][lane]);
+    lr[S] = next->lse[i][lane];
+  }
+  // Row a + i (slot R) into this wave's stash.
+  template <int R>
+  __device__ inline void stash(int i, int lane) {
+    mine->row[i][0][lane] = pack(kr[R]);
+    mine->row[i][1][lane] = pack(vr[R]);
+    mine->row[i][2][lane] = pack(qr[R]);
+    mine->row[i][3][lane] = pack(gr[R]);
+    mine->lse[i][lane] = lr[R];
+  }
+  __device__ static inline u32x4 pack(const Raw& r) { return u32x4{r.w[0], r.w[1], r.w[2], r.w[3]}; }
+  __device__ static inline Raw unpack(const u32x4& x) { return Raw{{x.x, x.y, x.z, x.w}}; }
 
   template <int R>
   __device__ inline void compute(int u) {
@@ -465,10 +487,26 @@ struct BwdFr4 {
       steps<R + 1>(u);
     }
   }
+  // steps() that also leave rows stash_from .. stash_from + 3 in the stash.
+  int stash_from;
+  template <int R>
+  __device__ inline void steps_stash(int u, int lane) {
+    if constexpr (R < RD) {
+      prefetch<(R + 1) % RD>(u + R + 1);
+      compute<R>(u + R);
+      const int i = u + R - stash_from;
+      if (i >= 0 && i < 4) stash<R>(i, lane);
+      steps_stash<R + 1>(u, lane);
+    }
+  }
 };
+
+// Tile sizes bwd_fr4's trip layout takes (see the kernel).
+constexpr bool fr4_layout_ok(int P) { return P >= 14 && (P + 4) % 6 == 0; }
 
 template <typename T, int LPR, int NM>
 __global__ __launch_bounds__(kPipeBlock) void bwd_fr4(Params p, WalkCfg c) {
+  __shared__ PipeStash stash_lds[kPipeWaves];
   WaveTile wt;
   wave_tile<LPR>(p, c, wt);
   constexpr int G = 64 / LPR, esz = (int)sizeof(T);
@@ -492,10 +530,83 @@ __global__ __launch_bounds__(kPipeBlock) void bwd_fr4(Params p, WalkCfg c) {
   w.last = wt.a + c.P + W::FR - 1;
   // Trips of RD steps from u0 (slot of u is (u - u0) % RD); the trip count
   // depends only on P.
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  // Halo rows from LDS: the four rows after the tile (steps a + P .. a + P + 3)
+  // are the first four rows of the next tile, which the next wave of the
+  // workgroup loads at its start (long gone from L2 when this wave gets
+  // there) and leaves in its stash.  The layout needs those steps to open the
+  // last trip, after at least two looped ones (P + 4 a multiple of RD, P >=
+  // 14: P = 32; the launch checks it).  At T = 2^20, layer 3: 1.40 -> 1.34 ms.
+  constexpr int RD = W::RD;
+  const int m = (c.P + 4) / RD;   // trip of step a + P
+  bool next_adj = false, has_prev = false;
+  {
+    const int64_t n = xcd_remap(blockIdx.x, gridDim.x, c.xs) * c.waves + wv;
+    int b2, hg2, a2;
+    if (wt.a < p.T && wv + 1 < c.waves && decode_tile(p, c, n + 1, b2, hg2, a2))
+      next_adj = b2 == wt.b && hg2 == wt.hg && a2 == wt.a + c.P;
+    if (wt.a < p.T && wv > 0 && decode_tile(p, c, n - 1, b2, hg2, a2))
+      has_prev = b2 == wt.b && hg2 == wt.hg && a2 + c.P == wt.a;
+  }
+  w.mine = &stash_lds[wv];
+  w.next = &stash_lds[wv + 1 < kPipeWaves ? wv + 1 : wv];
   w.template prefetch<0>(u0);
-  for (int u = u0; u <= w.last; u += W::RD) {
+  // Trips 0 .. m - 2; rows a .. a + 3 (steps 4 .. 7, in trips 0 and 1) also
+  // go to the stash when the wave before walks the tile before.
+  const int um = u0 + (m - 1) * RD;   // trip m - 1
+  w.stash_from = has_prev ? wt.a : wt.a + c.P + 8;   // past every step of the loop: no write
+  for (int u = u0; u < um; u += RD) {
     __syncthreads();
-    w.template steps<0>(u);
+    w.template steps_stash<0>(u, lane);
+  }
+  // Trips m - 1 and m (steps a + P .. a + P + 3 open trip m; its last two
+  // steps lie past the walk and are skipped).
+  const int ul = um + RD;
+  if (next_adj) {
+    __syncthreads();
+    w.template prefetch<1>(um + 1);
+    w.template compute<0>(um);
+    w.template prefetch<2>(um + 2);
+    w.template compute<1>(um + 1);
+    w.template prefetch<3>(um + 3);
+    w.template compute<2>(um + 2);
+    w.template prefetch<4>(um + 4);
+    w.template compute<3>(um + 3);
+    w.template prefetch<5>(um + 5);
+    w.template compute<4>(um + 4);
+    w.template prefetch_lds<0>(0, lane);
+    w.template compute<5>(um + 5);
+    __syncthreads();
+    w.template prefetch_lds<1>(1, lane);
+    w.template compute<0>(ul);
+    w.template prefetch_lds<2>(2, lane);
+    w.template compute<1>(ul + 1);
+    w.template prefetch_lds<3>(3, lane);
+    w.template compute<2>(ul + 2);
+    w.template compute<3>(ul + 3);
+  } else {
+    __syncthreads();
+    w.template prefetch<1>(um + 1);
+    w.template compute<0>(um);
+    w.template prefetch<2>(um + 2);
+    w.template compute<1>(um + 1);
+    w.template prefetch<3>(um + 3);
+    w.template compute<2>(um + 2);
+    w.template prefetch<4>(um + 4);
+    w.template compute<3>(um + 3);
+    w.template prefetch<5>(um + 5);
+    w.template compute<4>(um + 4);
+    w.template prefetch<0>(ul);
+    w.template compute<5>(um + 5);
+    __syncthreads();
+    w.template prefetch<1>(ul + 1);
+    w.template compute<0>(ul);
+    w.template prefetch<2>(ul + 2);
+    w.template compute<1>(ul + 1);
+    w.template prefetch<3>(ul + 3);
+    w.template compute<2>(ul + 2);
+    w.template compute<3>(ul + 3);
   }
 }
 
@@ -1118,8 +1229,10 @@ hipError_t launch_bwd(const Params& p, const WalkCfg& c, const Pattern& pat, int
       return pat.nm == 7 ? launch_chain<T, L, 7>(p, c, st) : launch_chain<T, L, 1>(p, c, st);
     const dim3 grid((unsigned)c.nwg), block(kPipeBlock);
     if (pat.far == 4 && !c.column) {
-      if (pat.nm == 7) hipLaunchKernelGGL((bwd_fr4<T, L, 7>), grid, block, kPipeLds, st, p, c);
-      else hipLaunchKernelGGL((bwd_fr4<T, L, 1>), grid, block, kPipeLds, st, p, c);
+      if (!fr4_layout_ok(c.P)) return hipErrorInvalidValue;
+      // Static LDS (the halo stash, 136 KiB) keeps one workgroup per CU.
+      if (pat.nm == 7) hipLaunchKernelGGL((bwd_fr4<T, L, 7>), grid, block, 0, st, p, c);
+      else hipLaunchKernelGGL((bwd_fr4<T, L, 1>), grid, block, 0, st, p, c);
       return hipGetLastError();
     }
     if (pat.far == 8 && !c.column)

@@ -90,14 +90,26 @@ struct ChainCfg {
   int xs;       // XCD stagger in workgroups (0: none; xcd_stagger)
 };
 
-// Rows this far apart (and more) get an XCD stagger of one eighth of an XCD's
-// range.  Without it the eight XCDs walk their ranges in step, each at the same
-// offset of its own range; measured at T = 2^20 (rows >= 16 MiB apart: F >=
-// 16384), the stagger took forwards 2-6% and backwards 2-12% faster (-0.6 ms
-// per step, two boxes), while at 1-8 MiB strides it cost the forward 2-4%.
+// XCD stagger of a column-order launch (column walks, chains), in workgroups,
+// by the far row stride (bytes between positions t and t + F).  Without it
+// the eight XCDs walk their ranges in step, each at the same offset of its
+// own range.  Measured at T = 2^20 (1 KiB rows, so F = stride / 1 KiB):
+//  * rows >= 16 MiB apart (F >= 16384): one eighth of an XCD's range, forwards
+//    2-6% and backwards 2-12% faster (-0.6 ms per step, two boxes);
+//  * 16 KiB - 1 MiB (F = 16 .. 512) forward and 16 KiB - 2 MiB (F = 16 ..
+//    1024) backward: one sixteenth (-0.11 to -0.14 ms per step in A/B runs
+//    against the build without it, mostly F = 128 .. 1024);
+//  * not at 1-16 MiB forward or 2-16 MiB backward, where every stagger tried
+//    (1/32 .. 1/2 of the range) cost up to 6% or did not hold in an A/B run.
 constexpr int64_t kStaggerStride = (int64_t)16 << 20;
-inline int xcd_stagger(int nwg, int64_t far_stride_bytes) {
-  return (nwg > 0 && nwg % 8 == 0 && far_stride_bytes >= kStaggerStride) ? nwg / 64 : 0;
+inline int xcd_stagger(int nwg, int64_t far_stride_bytes, bool fwd) {
+  if (nwg <= 0 || nwg % 8 != 0) return 0;
+  const int per = nwg / 8;
+  const int64_t fs = far_stride_bytes, KiB = 1024, MiB = KiB * KiB;
+  if (fs >= kStaggerStride) return per / 8;
+  if (fs < 16 * KiB) return 0;
+  if (fwd) return fs < MiB ? per / 16 : 0;
+  return fs < 2 * MiB ? per / 16 : 0;
 }
 
 // Row pairs (the plain backward): a workgroup of 8 waves holds chains of 2

@@ -117,7 +117,7 @@ WalkCfg launch_cfg(const Params& p, int dtype, const Pattern& pat, int lpr, bool
       c.rg = rg;
       order_tiles(p, pat, (int64_t)p.B * c.HG, c);
     }
-    c.xs = xcd_stagger(c.nwg, fs);
+    if (c.column) c.xs = xcd_stagger(c.nwg, fs, true);
     return c;
   }
   // The far-free forward takes 64-position tiles: its tiles load the 2 rows
@@ -144,8 +144,8 @@ WalkCfg launch_cfg(const Params& p, int dtype, const Pattern& pat, int lpr, bool
     order_tiles(p, pat, (int64_t)p.B * c.HG, c);
   }
   // The prologue walks keep the plain XCD order (the stagger was measured on
-  // the plain walks only).
-  if (!pro) c.xs = xcd_stagger(c.nwg, far_stride_bytes(p, pat, dtype));
+  // the plain walks only), and so do the linear layouts.
+  if (!pro && c.column) c.xs = xcd_stagger(c.nwg, far_stride_bytes(p, pat, dtype), fwd);
   return c;
 }
 

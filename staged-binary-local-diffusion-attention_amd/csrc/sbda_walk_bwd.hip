@@ -1189,7 +1189,7 @@ hipError_t launch_chain(const Params& p, const WalkCfg& wc, hipStream_t st) {
   const int64_t stride = p.q.st * (int64_t)sizeof(T);
   ChainCfg c = make_chain_cfg(p.B, stride, wc, chain_pairs_apply(wc, stride));
   if (c.nwg <= 0) return hipErrorInvalidValue;
-  c.xs = xcd_stagger(c.nwg, (int64_t)c.F * stride);
+  c.xs = xcd_stagger(c.nwg, (int64_t)c.F * stride, false);
   const dim3 grid((unsigned)c.nwg), block(64 * c.W);
   switch (c.W) {
     case 8: hipLaunchKernelGGL((bwd_chain<T, LPR, NM, 8>), grid, block, 0, st, p, c); break;

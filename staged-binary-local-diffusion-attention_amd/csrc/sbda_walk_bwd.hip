@@ -350,6 +350,7 @@ struct BwdFr4 {
   int T_, Tm1, a, end, last;
   PipeStash* mine;          // this wave's first four rows, for the wave before
   const PipeStash* next;    // the next wave's first four rows
+  int stash_from;           // first row to stash (past the loop's steps: none)
   Raw kr[RD], vr[RD], qr[RD], gr[RD];
   float lr[RD];
   float sp[RD][3], sd[RD][3];
@@ -479,16 +480,8 @@ struct BwdFr4 {
     }
   }
 
-  template <int R>
-  __device__ inline void steps(int u) {
-    if constexpr (R < RD) {
-      prefetch<(R + 1) % RD>(u + R + 1);
-      compute<R>(u + R);
-      steps<R + 1>(u);
-    }
-  }
-  // steps() that also leave rows stash_from .. stash_from + 3 in the stash.
-  int stash_from;
+  // Steps R .. RD - 1 of the trip from u (slot of u + R is R); the steps of
+  // rows stash_from .. stash_from + 3 also leave them in the stash.
   template <int R>
   __device__ inline void steps_stash(int u, int lane) {
     if constexpr (R < RD) {

@@ -100,16 +100,19 @@ WalkCfg launch_cfg(const Params& p, int dtype, const Pattern& pat, int lpr, bool
     // (Fewer than 4 bands: more rows per group, so no wave is left idle.)
     // Rows 4 MiB apart are the exception: pairs of 64-position rows that far
     // apart collide in the DRAM channel mapping, 8 rows x 1 band do not
-    // (layer 13 at T = 2^20: 1.01 -> 0.89 ms, two boxes).  From 8 MiB up, with
+    // (layer 13 at T = 2^20: 1.01 -> 0.89 ms, two boxes).  At 8 and 16 MiB, with
     // at least 4 rows, pairs of 32-position tiles (2 rows x 4 bands of 32)
-    // measured faster than 64 (layers 14-19: 0.76-0.80 against 0.75-0.87 ms,
-    // two boxes); not with 2 rows (layer 20: 0.80 against 0.74 ms).
+    // measured faster than 64 (layers 14-15: 0.75-0.78 against 0.77-0.79 ms);
+    // from 32 MiB up, with the XCD stagger, 64 is faster again (layers 16-19:
+    // 0.73-0.75 against 0.75-0.76 ms, two repetitions), and so it is with 2
+    // rows (layer 20: 0.80 against 0.74 ms before the stagger).
     // At F = 128, 64-position tiles leave 2 bands (a group of 4 rows x 2
     // bands); 32-position tiles keep the 2-row groups (layer 8: 0.787 against
     // 0.801 ms in the sweep below).
     const int64_t fs = far_stride_bytes(p, pat, dtype);
     const int64_t rows = (p.T + pat.far - 1) / pat.far;
-    const bool narrow = (fs >= ((int64_t)8 << 20) && rows >= 4) || pat.far < 4 * 64;
+    const bool narrow =
+        (fs >= ((int64_t)8 << 20) && fs < kBigStride && rows >= 4) || pat.far < 4 * 64;
     WalkCfg c = make_pipe_cfg(p, lpr, pat, narrow ? 32 : 64);
     if (c.column && c.rows >= 2) {
       int rg = (fs >= ((int64_t)4 << 20) && fs < ((int64_t)8 << 20)) ? 8 : 2;

@@ -87,7 +87,8 @@ struct ChainCfg {
   int blocks;   // row blocks (ceil(rows / L)) per band
   int bgroups;  // band groups (ceil(bands / (W / L)))
   int HG, nwg;
-  int xs;       // XCD stagger in workgroups (0: none; xcd_stagger)
+  int xs;         // XCD stagger in workgroups (0: none; xcd_stagger)
+  int band_fast;  // workgroup order: 1 band groups fastest, 0 row blocks fastest
 };
 
 // XCD stagger of a column-order launch (column walks, chains), in workgroups,

@@ -888,13 +888,22 @@ template <typename T, int LPR, int NM, int W>
 __global__ __launch_bounds__(64 * W) void bwd_chain(Params p, ChainCfg c) {
   __shared__ ChainSlot lds[W];
   const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  // Workgroup -> (batch, head group, band group, row block), XCD-contiguous;
-  // wave w -> row w % L of the block, band w / L of the group.
+  // Workgroup -> (batch, head group, band group, row block), XCD-contiguous,
+  // row blocks or band groups fastest; wave w -> row w % L of the block, band
+  // w / L of the group.
   int64_t g = xcd_remap(blockIdx.x, gridDim.x, c.xs);
-  const int rb = (int)(g % c.blocks);
-  g /= c.blocks;
-  const int bgi = (int)(g % c.bgroups);
-  g /= c.bgroups;
+  int rb, bgi;
+  if (c.band_fast) {
+    bgi = (int)(g % c.bgroups);
+    g /= c.bgroups;
+    rb = (int)(g % c.blocks);
+    g /= c.blocks;
+  } else {
+    rb = (int)(g % c.blocks);
+    g /= c.blocks;
+    bgi = (int)(g % c.bgroups);
+    g /= c.bgroups;
+  }
   const int hg = (int)(g % c.HG);
   const int b = (int)(g / c.HG);
   const int lr = w % c.L;
@@ -1180,9 +1189,18 @@ __global__ __launch_bounds__(64 * F) void bwd_tc(Params p, TcCfg cfg) {
 template <typename T, int LPR, int NM>
 hipError_t launch_chain(const Params& p, const WalkCfg& wc, hipStream_t st) {
   const int64_t stride = p.q.st * (int64_t)sizeof(T);
-  ChainCfg c = make_chain_cfg(p.B, stride, wc, chain_pairs_apply(wc, stride));
+  const bool pairs = chain_pairs_apply(wc, stride);
+  ChainCfg c = make_chain_cfg(p.B, stride, wc, pairs);
   if (c.nwg <= 0) return hipErrorInvalidValue;
-  c.xs = xcd_stagger(c.nwg, (int64_t)c.F * stride, false);
+  const int64_t fs = (int64_t)c.F * stride;
+  c.xs = xcd_stagger(c.nwg, fs, false);
+  // Row pairs at 1-4 MiB row strides take the band groups of a row block
+  // first: an XCD's workgroups then stream whole rows (contiguous memory)
+  // instead of the same columns of many rows.  At T = 2^20, layer 11 1.386 ->
+  // 1.362 ms and layer 12 1.496 -> 1.422 ms (two repetitions); at 512 KiB and
+  // from 4 MiB it measured equal or slower (layer 14: 1.42 -> 1.79 ms), and
+  // so did the forward's row groups (layer 12: 0.771 -> 0.785 ms).
+  c.band_fast = pairs && fs >= ((int64_t)1 << 20) && fs < ((int64_t)4 << 20);
   const dim3 grid((unsigned)c.nwg), block(64 * c.W);
   switch (c.W) {
     case 8: hipLaunchKernelGGL((bwd_chain<T, LPR, NM, 8>), grid, block, 0, st, p, c); break;

@@ -97,10 +97,11 @@ struct ChainCfg {
 // own range.  Measured at T = 2^20 (1 KiB rows, so F = stride / 1 KiB):
 //  * rows >= 16 MiB apart (F >= 16384): one eighth of an XCD's range, forwards
 //    2-6% and backwards 2-12% faster (-0.6 ms per step, two boxes);
-//  * 16 KiB - 1 MiB (F = 16 .. 512) forward and 16 KiB - 2 MiB (F = 16 ..
-//    1024) backward: one sixteenth (-0.11 to -0.14 ms per step in A/B runs
-//    against the build without it, mostly F = 128 .. 1024);
-//  * not at 1-16 MiB forward or 2-16 MiB backward, where every stagger tried
+//  * 16 KiB - 1 MiB (F = 16 .. 512) forward and 16 KiB - 4 MiB (F = 16 ..
+//    2048) backward: one sixteenth (-0.11 to -0.14 ms per step in A/B runs
+//    against the build without it, mostly F = 128 .. 1024; at F = 2048, with
+//    the row pairs' band-first order, -14 us);
+//  * not at 1-16 MiB forward or 4-16 MiB backward, where every stagger tried
 //    (1/32 .. 1/2 of the range) cost up to 6% or did not hold in an A/B run.
 constexpr int64_t kStaggerStride = (int64_t)16 << 20;
 inline int xcd_stagger(int nwg, int64_t far_stride_bytes, bool fwd) {
@@ -110,7 +111,7 @@ inline int xcd_stagger(int nwg, int64_t far_stride_bytes, bool fwd) {
   if (fs >= kStaggerStride) return per / 8;
   if (fs < 16 * KiB) return 0;
   if (fwd) return fs < MiB ? per / 16 : 0;
-  return fs < 2 * MiB ? per / 16 : 0;
+  return fs < 4 * MiB ? per / 16 : 0;
 }
 
 // Row pairs (the plain backward): a workgroup of 8 waves holds chains of 2

@@ -65,8 +65,8 @@ void order_tiles(const Params& p, const Pattern& pat, int64_t lanes_rows, WalkCf
 
 // Pipelined walks and the chained backward: lin_tile-position tiles in
 // linear order, or min(max_col_tile, F) for a power-of-two far offset F >= 16
-// (column order, far rows one column row away); halved (not below 16) while
-// the grid has fewer than 256 full workgroups.
+// (column order, far rows one column row away); halved (not below min_tile)
+// while the grid has fewer than 256 full workgroups.
 WalkCfg make_pipe_cfg(const Params& p, int lpr, const Pattern& pat, int max_col_tile,
                       int lin_tile = 32, int min_tile = 16) {
   WalkCfg c{};
@@ -104,8 +104,8 @@ WalkCfg launch_cfg(const Params& p, int dtype, const Pattern& pat, int lpr, bool
     // at least 4 rows, pairs of 32-position tiles (2 rows x 4 bands of 32)
     // measured faster than 64 (layers 14-15: 0.75-0.78 against 0.77-0.79 ms);
     // from 32 MiB up, with the XCD stagger, 64 is faster again (layers 16-19:
-    // 0.73-0.75 against 0.75-0.76 ms, two repetitions), and so it is with 2
-    // rows (layer 20: 0.80 against 0.74 ms before the stagger).
+    // 0.73-0.75 against 0.75-0.76 ms, two repetitions).  With 2 rows (layer
+    // 20) 64 was faster already (0.74 against 0.80 ms).
     // At F = 128, 64-position tiles leave 2 bands (a group of 4 rows x 2
     // bands); 32-position tiles keep the 2-row groups (layer 8: 0.787 against
     // 0.801 ms in the sweep below).
